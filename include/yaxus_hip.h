@@ -1,0 +1,117 @@
+/*
+ * yaxus_hip.h — the device half of yaxus's paged KV-cache path on MI355X (gfx950).
+ *
+ * These entry points are what a Rust FFI crate implementing yaxus's `Backend` trait
+ * (crates/yaxus-model/src/lib.rs:95-171) binds for the KV path:
+ *   Backend::new_kv      (lib.rs:118)  -> yx_kv_create
+ *   Backend::copy_page   (lib.rs:120)  -> yx_kv_copy_pages (a batch of PageCopy, kv.rs:35)
+ *   Backend::begin_pass  (lib.rs:123)  -> yx_pass_begin    (PassMeta, lib.rs:63-89)
+ *   Backend::attention   (lib.rs:132)  -> yx_kv_append (+ yx_attention); the K/V store
+ *                                          of write_rows (backend-cpu lib.rs:378-383)
+ *                                          and attend (backend-cpu lib.rs:389-427)
+ *
+ * Conventions: int status, YX_OK = 0 (codes shared with yaxus_kv_cache.h);
+ * yx_last_error() returns a thread-local message; no exception crosses the ABI. Every
+ * call takes a context; all device work goes, in call order, on the context's one HIP
+ * stream. Calls whose pointers are host pointers are synchronous; the `_dev` variants
+ * take device pointers and are asynchronous (yx_sync waits).
+ *
+ * The arena layout is private: per layer, K and V are `[page][kv_head][page_size][128]`
+ * IEEE binary16, so one (page, kv head) is one contiguous block. head_dim is 128 (the
+ * reference GPU kernels are written for 128 as well: yaxus-backend-gpu lib.rs:72).
+ */
+#ifndef YAXUS_HIP_H
+#define YAXUS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "yaxus_kv_cache.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct yx_ctx yx_ctx;
+typedef struct yx_kv yx_kv;
+
+enum { YX_DTYPE_F32 = 0, YX_DTYPE_F16 = 1 };
+enum { YX_K = 0, YX_V = 1 };
+/* Kernels whose launches yx_profile_read reports. */
+enum { YX_KERNEL_ATTENTION = 0, YX_KERNEL_APPEND = 1, YX_KERNEL_COPY = 2 };
+
+const char* yx_last_error(void);
+int yx_device_count(int* n);
+
+/* A context: one device, one stream, the current pass's metadata and the scratch
+ * space of the attention (split-K partials and arrival counters). */
+int yx_ctx_create(int device, yx_ctx** out);
+int yx_ctx_destroy(yx_ctx* ctx);
+int yx_sync(yx_ctx* ctx);
+/* Tuning knobs: "attn_target_waves" (split-K work items aimed at per launch),
+ * "attn_max_chunk_blocks" (most 16-key blocks per work item). */
+int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
+
+/* Backend::new_kv (lib.rs:118; GPU ops/mod.rs:42-66): `layers` layers of `pages`
+ * pages of `page_size` tokens (a multiple of 16). dtype YX_DTYPE_F16 only. Zeroed. */
+int yx_kv_create(yx_ctx* ctx, size_t layers, size_t pages, size_t page_size, size_t hkv,
+                 size_t head_dim, int dtype, yx_kv** out);
+int yx_kv_destroy(yx_ctx* ctx, yx_kv* kv);
+/* Device pointer of one layer's K or V arena (for fills and device-side tools). */
+int yx_kv_layer_ptr(yx_kv* kv, size_t layer, int which, void** out);
+size_t yx_kv_page_bytes(const yx_kv* kv);
+
+/* Backend::copy_page (lib.rs:120; CPU lib.rs:472-479), batched: page src[i] -> dst[i]
+ * in every layer, K and V, in list order (a later copy sees an earlier one's result). */
+int yx_kv_copy_pages(yx_ctx* ctx, yx_kv* kv, const uint32_t* src, const uint32_t* dst, size_t n);
+
+/* Raw page contents, `[n][hkv][page_size][128]` binary16 bits, synchronous. */
+int yx_kv_read_pages(yx_ctx* ctx, yx_kv* kv, size_t layer, const uint32_t* pages, size_t n,
+                     void* k_out, void* v_out);
+int yx_kv_write_pages(yx_ctx* ctx, yx_kv* kv, size_t layer, const uint32_t* pages, size_t n,
+                      const void* k_in, const void* v_in);
+
+/* Backend::begin_pass (lib.rs:123; GPU ops/mod.rs:76-99): the rows of the next pass.
+ * Rows of one sequence are consecutive, share pt_off and have consecutive positions. */
+int yx_pass_begin(yx_ctx* ctx, size_t rows, const uint32_t* pos, const uint32_t* kv_slot,
+                  const uint32_t* pt_off, const uint32_t* pages, size_t npages);
+
+/* The K/V store of write_rows (backend-cpu lib.rs:378-383; QK_ROPE's store,
+ * yaxus-backend-gpu shaders.rs:285-341): k and v are `[rows][hkv][128]` f32, rounded
+ * to binary16 (nearest-even) and scattered to each row's kv_slot of `layer`. */
+int yx_kv_append(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k, const float* v);
+int yx_kv_append_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k, const float* v);
+
+/* attend (backend-cpu lib.rs:389-427; ATTN_SPLIT + ATTN_COMBINE, shaders.rs:1466-1637):
+ * causal GQA attention of q `[rows][hq][128]` f32 over each row's keys `[lo, pos]`,
+ * lo = pos + 1 - window when window > 0 and pos + 1 > window, else 0. out is
+ * `[rows][hq][128]` f32. `scale` multiplies q.k (the reference uses 1/sqrt(128)). */
+int yx_attention(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* q, float* out, size_t hq,
+                 size_t hkv, size_t window, float scale);
+int yx_attention_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* q, float* out,
+                     size_t hq, size_t hkv, size_t window, float scale);
+
+/* Device memory and copies on the context's stream (h2d/d2h are synchronous). */
+int yx_dev_alloc(yx_ctx* ctx, size_t bytes, void** out);
+int yx_dev_free(yx_ctx* ctx, void* p);
+int yx_memcpy_h2d(yx_ctx* ctx, void* dst, const void* src, size_t bytes);
+int yx_memcpy_d2h(yx_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Plain device copy kernel (also the reference point for HBM byte counters). */
+int yx_dev_copy(yx_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Synthetic N(0,1) values: splitmix64 -> Box-Muller, element i of stream `seed` at
+ * index offset + i (see yaxus_amd/data.py for the definition); dtype f32 or f16. */
+int yx_fill_normal(yx_ctx* ctx, void* dst, size_t n, int dtype, uint64_t seed, uint64_t offset);
+
+/* Timing with HIP events on the context's stream. */
+int yx_timer_start(yx_ctx* ctx);
+int yx_timer_stop(yx_ctx* ctx, float* ms);
+/* When on, every launch of the kernels above is bracketed by an event pair;
+ * yx_profile_read waits, returns the summed duration and launch count of one kernel
+ * since the last read, and resets them. */
+int yx_profile_enable(yx_ctx* ctx, int on);
+int yx_profile_read(yx_ctx* ctx, int kernel, double* total_ms, uint64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,131 @@
+"""GPU parity of the KV path against the CPU oracle (through the C ABI).
+
+Bit-exact: appended K/V bytes, page copies. Tolerance (2e-3 abs + 1e-3 rel, f16 KV
+with f32 accumulation): attention outputs vs the f32 restatement of
+`LayerPass::attend` (crates/yaxus-backend-cpu/src/lib.rs:389-427) on the same f16 K/V.
+"""
+
+import numpy as np
+import pytest
+
+from tests.scenario import D, Scenario, close
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_pages(sc, layer, pages):
+    k, v = sc.kv.read_pages(layer, pages)
+    for i, p in enumerate(pages):
+        ok, ov = sc.orc[layer].page_bits(p)
+        assert np.array_equal(k[i], ok), f"K bits differ on page {p}"
+        assert np.array_equal(v[i], ov), f"V bits differ on page {p}"
+
+
+def test_append_is_bit_exact(hip):
+    sc = Scenario(hip, pages=64, page=16, hkv=4, pool_seed=3)
+    a, b = sc.cache.new_seq(), sc.cache.new_seq()
+    sc.prefill({a: 37, b: 70})
+    used = sorted(set(sc.cache.seq_pages(a)) | set(sc.cache.seq_pages(b)))
+    _check_pages(sc, 0, used)
+
+
+def test_append_rounds_special_values(hip):
+    """Round-to-nearest-even ties, subnormals, overflow and signed zeros."""
+    from oracle.attn import f32_to_f16_bits
+
+    sc = Scenario(hip, pages=4, page=16, hkv=1)
+    s = sc.cache.new_seq()
+    pr = sc.run_pass([(s, 16)])
+    vals = np.array([0.0, -0.0, 1.0, 65504.0, 65520.0, 65519.99, 1e-8, -1e-8, 2.0 ** -24,
+                     2.0 ** -25, 3 * 2.0 ** -25, 2.0 ** -14, 1.00048828125, 1.00146484375,
+                     -2.5e-6, 6e-5], np.float32)
+    rng = np.random.default_rng(0)
+    k = rng.standard_normal((16, 1, D)).astype(np.float32) * np.float32(3e-5)
+    k[:, 0, :16] = vals
+    v = (rng.standard_normal((16, 1, D)) * 1e4).astype(np.float32)
+    hip.append(sc.kv, 0, k, v)
+    kb, vb = sc.kv.read_pages(0, [int(pr.meta.pages[0])])
+    assert np.array_equal(kb[0, 0], f32_to_f16_bits(k[:, 0, :]))
+    assert np.array_equal(vb[0, 0], f32_to_f16_bits(v[:, 0, :]))
+    assert np.array_equal(f32_to_f16_bits(vals), vals.astype(np.float16).view(np.uint16))
+
+
+def test_copy_pages_in_order(hip):
+    sc = Scenario(hip, pages=8, page=16, hkv=2, layers=2)
+    s = sc.cache.new_seq()
+    sc.prefill({s: 5 * 16})
+    from yaxus_amd import PageCopy
+
+    # A chain: 0 -> 5, then 5 -> 6 must see the first copy's result; 1 -> 0 after 0 is read.
+    copies = [PageCopy(0, 5), PageCopy(5, 6), PageCopy(1, 0)]
+    hip.copy_pages(sc.kv, copies)
+    for c in copies:
+        for o in sc.orc:
+            o.copy_page(c.src, c.dst)
+    for layer in range(2):
+        _check_pages(sc, layer, list(range(8)))
+
+
+@pytest.mark.parametrize("page", [16, 128])
+@pytest.mark.parametrize("window", [0, 100])
+def test_decode_matches_oracle(hip, page, window):
+    hq, hkv = 16, 4
+    sc = Scenario(hip, pages=256 if page == 16 else 48, page=page, hkv=hkv, pool_seed=11)
+    lens = [1, 15, 16, 17, 300, 1000, 33, 250]
+    seqs = [sc.cache.new_seq() for _ in lens]
+    sc.prefill(dict(zip(seqs, lens)))
+    pr = sc.run_pass([(s, 1) for s in seqs])
+    sc.store(pr)
+    rows = len(seqs)
+    q = sc.draw(rows * hq * D).reshape(rows, hq * D)
+    got = hip.attend(sc.kv, 0, q, hq, window=window)
+    want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
+    err = np.abs(got - want).max()
+    assert close(got, want).all(), f"max abs err {err}"
+
+
+@pytest.mark.parametrize("target_waves", [1, 64, 4096])
+def test_split_count_does_not_change_results(hip, target_waves):
+    hq, hkv = 8, 2
+    sc = Scenario(hip, pages=160, page=16, hkv=hkv, pool_seed=5)
+    seqs = [sc.cache.new_seq() for _ in range(3)]
+    sc.prefill(dict(zip(seqs, [700, 1200, 64])))
+    pr = sc.run_pass([(s, 1) for s in seqs])
+    sc.store(pr)
+    q = sc.draw(3 * hq * D).reshape(3, hq * D)
+    hip.set_option("attn_target_waves", target_waves)
+    try:
+        got = hip.attend(sc.kv, 0, q, hq)
+    finally:
+        hip.set_option("attn_target_waves", 2048)
+    want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
+    assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
+
+
+@pytest.mark.parametrize("hq,hkv,k", [(16, 4, 6), (16, 4, 5), (8, 8, 3), (16, 1, 2), (32, 1, 1)])
+def test_verify_rows_are_causal(hip, hq, hkv, k):
+    """Multi-row passes per sequence (speculative verify): rows see keys <= their pos."""
+    sc = Scenario(hip, pages=128, page=16, hkv=hkv, pool_seed=9)
+    seqs = [sc.cache.new_seq() for _ in range(4)]
+    sc.prefill(dict(zip(seqs, [40, 513, 7, 260])))
+    pr = sc.run_pass([(s, k) for s in seqs])
+    sc.store(pr)
+    rows = len(pr.meta.pos)
+    q = sc.draw(rows * hq * D).reshape(rows, hq * D)
+    got = hip.attend(sc.kv, 0, q, hq, window=0)
+    want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
+    assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
+
+
+def test_attention_close_to_f64(hip):
+    """The device result is closer to the f64 brute force than the tolerance by far."""
+    hq, hkv = 16, 4
+    sc = Scenario(hip, pages=400, page=16, hkv=hkv, pool_seed=2)
+    seqs = [sc.cache.new_seq() for _ in range(4)]
+    sc.prefill(dict(zip(seqs, [4095, 2000, 17, 1])))
+    pr = sc.run_pass([(s, 1) for s in seqs])
+    sc.store(pr)
+    q = sc.draw(4 * hq * D).reshape(4, hq * D)
+    got = hip.attend(sc.kv, 0, q, hq)
+    exact = sc.orc[0].attend_f64(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
+    assert np.abs(got - exact).max() < 2e-5

@@ -1,0 +1,199 @@
+"""The HIP backend of the KV path: the part of yaxus's ``Backend`` trait that touches
+the KV arena (crates/yaxus-model/src/lib.rs:95-171), over ``libyaxus_hip.so``.
+
+    Backend::new_kv      (lib.rs:118)  -> HipBackend.new_kv
+    Backend::copy_page   (lib.rs:120)  -> HipBackend.copy_page / copy_pages
+    Backend::begin_pass  (lib.rs:123)  -> HipBackend.begin_pass
+    Backend::attention   (lib.rs:132)  -> HipBackend.append (the K/V store of
+                                          write_rows) + HipBackend.attend
+
+Tensors are ``DeviceTensor`` values (device memory owned by the context); numpy arrays
+are accepted where a host round trip is intended. A missing library, or a context
+that cannot open a gfx950 device, raises: nothing here computes on the host.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import check_hip, ptr
+
+
+class DeviceTensor:
+    """A device buffer of a fixed numpy dtype and shape, freed with its context."""
+
+    def __init__(self, backend, shape, dtype):
+        self.backend = backend
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = ctypes.c_void_p()
+        check_hip(backend.L.yx_dev_alloc(backend.ctx, max(self.nbytes, 16), ctypes.byref(p)))
+        self.ptr = p
+
+    def upload(self, a):
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        if a.nbytes != self.nbytes:
+            raise ValueError(f"upload of {a.nbytes} bytes into {self.nbytes}")
+        check_hip(self.backend.L.yx_memcpy_h2d(self.backend.ctx, self.ptr, ptr(a), self.nbytes))
+        return self
+
+    def numpy(self):
+        out = np.empty(self.shape, dtype=self.dtype)
+        check_hip(self.backend.L.yx_memcpy_d2h(self.backend.ctx, ptr(out), self.ptr, self.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.backend.L.yx_dev_free(self.backend.ctx, self.ptr)
+            self.ptr = None
+
+
+class Kv:
+    """The arena of one model: ``layers`` layers of ``pages`` pages (binary16 K/V)."""
+
+    def __init__(self, backend, handle, layers, pages, page, hkv, d):
+        self.backend, self.h = backend, handle
+        self.layers, self.pages, self.page, self.hkv, self.d = layers, pages, page, hkv, d
+
+    def layer_ptr(self, layer, which):
+        p = ctypes.c_void_p()
+        check_hip(self.backend.L.yx_kv_layer_ptr(self.h, layer, which, ctypes.byref(p)))
+        return p
+
+    @property
+    def page_bytes(self):
+        return self.backend.L.yx_kv_page_bytes(self.h)
+
+    def read_pages(self, layer, pages):
+        """(K, V) bits of the pages, each ``[n][hkv][page][d]`` uint16."""
+        pg = np.ascontiguousarray(pages, dtype=np.uint32)
+        k = np.empty((len(pg), self.hkv, self.page, self.d), np.uint16)
+        v = np.empty_like(k)
+        check_hip(self.backend.L.yx_kv_read_pages(self.backend.ctx, self.h, layer, ptr(pg),
+                                                  len(pg), ptr(k), ptr(v)))
+        return k, v
+
+    def write_pages(self, layer, pages, k, v):
+        pg = np.ascontiguousarray(pages, dtype=np.uint32)
+        k = np.ascontiguousarray(k, dtype=np.uint16)
+        v = np.ascontiguousarray(v, dtype=np.uint16)
+        check_hip(self.backend.L.yx_kv_write_pages(self.backend.ctx, self.h, layer, ptr(pg),
+                                                   len(pg), ptr(k), ptr(v)))
+
+    def destroy(self):
+        if self.h:
+            self.backend.L.yx_kv_destroy(self.backend.ctx, self.h)
+            self.h = None
+
+
+class HipBackend:
+    """One device context (one HIP stream) and the KV path's operations on it."""
+
+    def __init__(self, device=0):
+        self.L = _lib.hip_lib()
+        c = ctypes.c_void_p()
+        check_hip(self.L.yx_ctx_create(device, ctypes.byref(c)))
+        self.ctx = c
+        self.rows = 0
+
+    def name(self):
+        return "hip (gfx950)"
+
+    def close(self):
+        if self.ctx:
+            self.L.yx_ctx_destroy(self.ctx)
+            self.ctx = None
+
+    def set_option(self, key, value):
+        check_hip(self.L.yx_ctx_set_option(self.ctx, key.encode(), int(value)))
+
+    def sync(self):
+        check_hip(self.L.yx_sync(self.ctx))
+
+    def tensor(self, shape, dtype=np.float32):
+        return DeviceTensor(self, shape, dtype)
+
+    # Backend::new_kv (lib.rs:118)
+    def new_kv(self, layers, pages, page, hkv, d=128):
+        h = ctypes.c_void_p()
+        check_hip(self.L.yx_kv_create(self.ctx, layers, pages, page, hkv, d, _lib.YX_DTYPE_F16,
+                                      ctypes.byref(h)))
+        return Kv(self, h, layers, pages, page, hkv, d)
+
+    # Backend::copy_page (lib.rs:120), batched in list order
+    def copy_pages(self, kv, copies):
+        if not copies:
+            return
+        src = np.array([c.src for c in copies], np.uint32)
+        dst = np.array([c.dst for c in copies], np.uint32)
+        check_hip(self.L.yx_kv_copy_pages(self.ctx, kv.h, ptr(src), ptr(dst), len(src)))
+
+    def copy_page(self, kv, src, dst):
+        s = np.array([src], np.uint32)
+        d = np.array([dst], np.uint32)
+        check_hip(self.L.yx_kv_copy_pages(self.ctx, kv.h, ptr(s), ptr(d), 1))
+
+    # Backend::begin_pass (lib.rs:123)
+    def begin_pass(self, meta):
+        pos = np.ascontiguousarray(meta.pos, np.uint32)
+        slot = np.ascontiguousarray(meta.kv_slot, np.uint32)
+        off = np.ascontiguousarray(meta.pt_off, np.uint32)
+        pages = np.ascontiguousarray(meta.pages, np.uint32)
+        check_hip(self.L.yx_pass_begin(self.ctx, len(pos), ptr(pos), ptr(slot), ptr(off),
+                                       ptr(pages), len(pages)))
+        self.rows = len(pos)
+        self._keep = (pos, slot, off, pages)
+
+    # The K/V store of Backend::attention (backend-cpu lib.rs:378-383)
+    def append(self, kv, layer, k, v):
+        if isinstance(k, DeviceTensor):
+            check_hip(self.L.yx_kv_append_dev(self.ctx, kv.h, layer, k.ptr, v.ptr))
+            return
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        if k.size != self.rows * kv.hkv * kv.d or v.size != k.size:
+            raise ValueError("k/v must be [rows][hkv][head_dim] f32")
+        check_hip(self.L.yx_kv_append(self.ctx, kv.h, layer, ptr(k), ptr(v)))
+
+    # The attend half of Backend::attention (backend-cpu lib.rs:389-427)
+    def attend(self, kv, layer, q, hq, window=None, scale=None, out=None):
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(kv.d))) if scale is None else scale
+        w = int(window or 0)
+        if isinstance(q, DeviceTensor):
+            out = out if out is not None else self.tensor((self.rows, hq * kv.d))
+            check_hip(self.L.yx_attention_dev(self.ctx, kv.h, layer, q.ptr, out.ptr, hq, kv.hkv,
+                                              w, scale))
+            return out
+        q = np.ascontiguousarray(q, np.float32)
+        if q.size != self.rows * hq * kv.d:
+            raise ValueError("q must be [rows][hq][head_dim] f32")
+        o = np.empty((self.rows, hq * kv.d), np.float32)
+        check_hip(self.L.yx_attention(self.ctx, kv.h, layer, ptr(q), ptr(o), hq, kv.hkv, w,
+                                      scale))
+        return o
+
+    def fill_normal(self, dev_ptr, n, f16, seed, offset=0):
+        check_hip(self.L.yx_fill_normal(self.ctx, dev_ptr, n,
+                                        _lib.YX_DTYPE_F16 if f16 else _lib.YX_DTYPE_F32,
+                                        seed, offset))
+
+    def timer_start(self):
+        check_hip(self.L.yx_timer_start(self.ctx))
+
+    def timer_stop(self):
+        ms = ctypes.c_float()
+        check_hip(self.L.yx_timer_stop(self.ctx, ctypes.byref(ms)))
+        return ms.value
+
+    def profile(self, on):
+        check_hip(self.L.yx_profile_enable(self.ctx, 1 if on else 0))
+
+    def profile_read(self, kernel):
+        t = ctypes.c_double()
+        n = ctypes.c_uint64()
+        check_hip(self.L.yx_profile_read(self.ctx, kernel, ctypes.byref(t), ctypes.byref(n)))
+        return t.value, n.value

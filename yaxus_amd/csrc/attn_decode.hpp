@@ -1,0 +1,375 @@
+// Paged decode / verify attention for gfx950 (wave64, MFMA).
+//
+// Restates the arithmetic of `LayerPass::attend` (crates/yaxus-backend-cpu/src/
+// lib.rs:389-427): per (row, query head), keys `[lo, pos]` of the row's sequence
+// through its page table, softmax of q.k * scale, and the weighted sum of V. The
+// reference GPU splits keys into chunks and merges them afterwards (ATTN_SPLIT +
+// ATTN_COMBINE, crates/yaxus-backend-gpu/src/shaders.rs:1466-1637); here too, but the
+// merge is done by the last work item of a (rows, kv head) to finish, in chunk order.
+//
+// One workgroup of 4 waves per work item = (a group of consecutive rows of one
+// sequence, one KV head, one chunk of 16-key blocks); its waves split the chunk's
+// blocks and merge through LDS. The group's (row, query head) pairs are "logical rows";
+// NT tiles of 8 logical rows each are kept in MFMA columns as an f16 hi part
+// (columns 0-7) and an f16 lo part (columns 8-15) of q, so q.k is accurate to ~2^-22
+// relative with f16 K exact and f32 accumulation. Per block of 16 keys:
+//   S^T[key][col] = K[key][:] . Q[col][:]   4 x v_mfma_f32_16x16x32_f16
+//   online softmax per column; P = exp2(S*scale*log2e - m) split into hi/lo f16
+//   O^T[dim][col] += V^T[dim][key] P^T[key][col]   8 x v_mfma_f32_16x16x16_f16
+// K is the A operand with lane l holding key l%16, dims p*32 + (l/16)*8 + 0..7 for
+// MFMA p: each lane's 16-byte load reads 16 consecutive bytes of one key row. V is the
+// A operand of the PV product with lane l holding dims (l%16)*8 + j for 4 keys, so
+// each V load is a row-contiguous 16 bytes too and the output lands as 32 consecutive
+// dims of one column per lane.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace yx {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// One split-K work item (host-built, see runtime.hip).
+struct AttnItem {
+  uint32_t r0;         // first pass row of the group
+  uint32_t nrows;      // rows in the group
+  uint32_t pt_off;     // offset of the group's page table in the pass's pages
+  uint32_t blk0;       // first 16-key block (absolute key / 16) of this chunk
+  uint32_t blk1;       // one past the last block of this chunk
+  uint32_t chunk;      // chunk index within the group
+  uint32_t nch;        // chunks of the group
+  uint32_t part_base;  // first partial slot of the group
+  uint32_t counter;    // arrival counter index of the group
+  uint32_t pad[3];
+};
+
+static constexpr float kLog2e = 1.4426950408889634f;
+static constexpr int kD = 128;
+
+// Lane l reads lane l^8 (DPP row rotate by 8 within each row of 16 lanes).
+__device__ __forceinline__ float xor8(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+}
+// Lane l reads lane l^16 (swizzle, bit-mask mode: and 0x1f, or 0, xor 0x10).
+__device__ __forceinline__ float xor16(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
+}
+
+// K/V of one 16-key block held by a lane (see the header comment for the mapping).
+struct BlockRegs {
+  half8 k[4];
+  half8 v[4];
+};
+
+__device__ __forceinline__ void load_block(BlockRegs& r, const _Float16* __restrict__ kbase,
+                                           const _Float16* __restrict__ vbase, int lane) {
+  const int c = lane & 15, g = lane >> 4;
+  const half8* kp = reinterpret_cast<const half8*>(kbase + c * kD + g * 8);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) r.k[p] = __builtin_nontemporal_load(kp + p * 4);
+  const half8* vp = reinterpret_cast<const half8*>(vbase + (4 * g) * kD + c * 8);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.v[i] = __builtin_nontemporal_load(vp + i * (kD / 8));
+}
+
+// Write-through 16-byte store / coherent load of split-K partials through a buffer
+// resource with the sc1 cache policy: the data goes to (and comes from) the memory
+// all XCDs share, so the hand-off between workgroups needs no L2 write-back.
+static constexpr int kCoherent = 16;  // sc1
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(p, 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ void st4_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, float4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, static_cast<int>(off), 0, kCoherent);
+}
+__device__ __forceinline__ float4 ld4_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, kCoherent));
+}
+__device__ __forceinline__ void st2_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, float2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(uint32_t __attribute__((ext_vector_type(2))), v), r,
+                                        static_cast<int>(off), 0, kCoherent);
+}
+__device__ __forceinline__ float2 ld2_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, kCoherent));
+}
+
+// Waves per workgroup: they share one work item's blocks and merge through LDS.
+static constexpr int kWaves = 4;
+
+template <int NT>
+struct DecodeShared {
+  float m[kWaves][NT * 8];
+  float l[kWaves][NT * 8];
+  float4 o[kWaves][NT * 8][kD / 4];
+  uint32_t last;
+};
+
+template <int NT>
+__global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
+    const AttnItem* __restrict__ items, const uint32_t* __restrict__ pos,
+    const uint32_t* __restrict__ pages, const _Float16* __restrict__ kc,
+    const _Float16* __restrict__ vc, const float* __restrict__ q, float* __restrict__ out,
+    float* __restrict__ part_o, float2* __restrict__ part_ml, uint32_t* __restrict__ counters,
+    uint32_t part_o_bytes, uint32_t part_ml_bytes, uint32_t hq, uint32_t hkv,
+    uint32_t bpp_shift, uint32_t window, float scale_log2) {
+  __shared__ DecodeShared<NT> sh;
+  const AttnItem it = items[blockIdx.x];
+  const uint32_t kh = blockIdx.y;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, g = lane >> 4;
+  const bool lo_half = c >= 8;
+  const uint32_t G = hq / hkv;
+  const uint32_t nlog = it.nrows * G;  // logical rows in the group
+
+  // Per tile: this lane's column's row position and key window, and the q operand.
+  half8 qb[NT][4];
+  int rpos[NT], rlo[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const uint32_t lr = t * 8 + (c & 7);
+    rpos[t] = -1;
+    rlo[t] = 0;
+    if (lr < nlog) {
+      const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
+      const int p = static_cast<int>(pos[rr]);
+      rpos[t] = p;
+      rlo[t] = (window > 0 && p + 1 > static_cast<int>(window)) ? p + 1 - static_cast<int>(window) : 0;
+      const float* qp = q + (static_cast<size_t>(rr) * hq + h) * kD + g * 8;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const float4 a = *reinterpret_cast<const float4*>(qp + pp * 32);
+        const float4 b = *reinterpret_cast<const float4*>(qp + pp * 32 + 4);
+        const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const _Float16 hi = static_cast<_Float16>(x[e]);
+          qb[t][pp][e] = lo_half ? static_cast<_Float16>(x[e] - static_cast<float>(hi)) : hi;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) qb[t][pp] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+
+  float m[NT], l[NT];
+  floatx4 acc[NT][8];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    m[t] = -INFINITY;
+    l[t] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[t][j] = floatx4{0, 0, 0, 0};
+  }
+
+  // This wave's share of the work item's blocks: [wb0, wb1), at most 64 of them.
+  const uint32_t nall = it.blk1 - it.blk0;
+  const uint32_t wb0 = it.blk0 + nall * wave / kWaves;
+  const uint32_t wb1 = it.blk0 + nall * (wave + 1) / kWaves;
+  const uint32_t nblk = wb1 - wb0;
+  // Page ids of those blocks, one per lane; block b reads its page back with readlane.
+  const uint32_t bpp_mask = (1u << bpp_shift) - 1u;  // blocks per page - 1
+  const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;  // halves per (page, head)
+  const uint32_t* pt = pages + it.pt_off;
+  int pid = 0;
+  if (static_cast<uint32_t>(lane) < nblk) pid = static_cast<int>(pt[(wb0 + lane) >> bpp_shift]);
+  auto block_off = [&](uint32_t b) -> size_t {  // b relative to wb0, clamped
+    b = b < nblk ? b : nblk - 1;
+    const uint32_t page = static_cast<uint32_t>(__builtin_amdgcn_readlane(pid, static_cast<int>(b)));
+    return (static_cast<size_t>(page) * hkv + kh) * head_stride +
+           static_cast<size_t>((wb0 + b) & bpp_mask) * 16 * kD;
+  };
+  const int key_end = static_cast<int>(wb1 * 16);
+
+  // Two register sets of two blocks each, used in turn: the loads of one set are in
+  // flight while the other is computed.
+  BlockRegs s0[2], s1[2];
+  auto load_pair = [&](BlockRegs* r, uint32_t b) {
+    const size_t o0 = block_off(b), o1 = block_off(b + 1);
+    load_block(r[0], kc + o0, vc + o0, lane);
+    load_block(r[1], kc + o1, vc + o1, lane);
+    // Keep the loads here: the scheduler would otherwise sink them below the compute
+    // of the other set, leaving nothing in flight while it runs.
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto process_pair = [&](const BlockRegs* r, uint32_t b) {
+    const int kb0 = static_cast<int>((wb0 + b) * 16) + 4 * g;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float x[8];
+      float bmax = -INFINITY;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        floatx4 sc = {0, 0, 0, 0};
+#pragma unroll
+        for (int p = 0; p < 4; ++p) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r[h].k[p], qb[t][p], sc, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float full = sc[i] + xor8(sc[i]);
+          const int kp = kb0 + h * 16 + i;
+          const bool ok = kp >= rlo[t] && kp <= rpos[t] && kp < key_end;
+          x[h * 4 + i] = ok ? full * scale_log2 : -INFINITY;
+          bmax = fmaxf(bmax, x[h * 4 + i]);
+        }
+      }
+      bmax = fmaxf(bmax, xor16(bmax));
+      bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+      const float mn = fmaxf(m[t], bmax);
+      const bool live = mn != -INFINITY;
+      const float corr = live ? __builtin_amdgcn_exp2f(m[t] - mn) : 1.0f;
+      float pr[8], rs = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        pr[i] = live ? __builtin_amdgcn_exp2f(x[i] - mn) : 0.0f;
+        rs += pr[i];
+      }
+      rs += xor16(rs);
+      rs += __shfl_xor(rs, 32);
+      l[t] = l[t] * corr + rs;
+      m[t] = mn;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[t][j] *= corr;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        half4 pb;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pv = pr[h * 4 + i];
+          const _Float16 hi = static_cast<_Float16>(pv);
+          pb[i] = lo_half ? static_cast<_Float16>(pv - static_cast<float>(hi)) : hi;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const half4 a = {r[h].v[0][j], r[h].v[1][j], r[h].v[2][j], r[h].v[3][j]};
+          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, acc[t][j], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  if (nblk > 0) {
+    // Loads are issued unconditionally (past the end they re-read the last block) so
+    // that every path through the loop has the same loads outstanding and the waits
+    // before each use stay partial.
+    load_pair(s0, 0);
+    for (uint32_t b = 0; b < nblk; b += 4) {
+      load_pair(s1, b + 2);
+      process_pair(s0, b);
+      load_pair(s0, b + 4);
+      if (b + 2 < nblk) process_pair(s1, b + 2);
+    }
+  }
+
+  // Join the hi and lo columns (lanes c and c^8 hold the same logical row), then hand
+  // each wave's (m, l, O) of its logical rows to LDS.
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[t][j][i] += xor8(acc[t][j][i]);
+    const int lr = t * 8 + c;
+    if (c < 8) {
+      if (g == 0) {
+        sh.m[wave][lr] = m[t];
+        sh.l[wave][lr] = l[t];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sh.o[wave][lr][g * 8 + i * 2] = float4{acc[t][0][i], acc[t][1][i], acc[t][2][i], acc[t][3][i]};
+        sh.o[wave][lr][g * 8 + i * 2 + 1] = float4{acc[t][4][i], acc[t][5][i], acc[t][6][i], acc[t][7][i]};
+      }
+    }
+  }
+  __syncthreads();
+
+  // Merge the waves: thread -> (row, 4 dims); NT*8 rows x 32 quads = NT * 256 values.
+  const size_t qd = static_cast<size_t>(hq) * kD;
+  const uint32_t rows_per_slot = NT * 8;
+  const size_t slot = (static_cast<size_t>(it.part_base) + it.chunk) * hkv + kh;
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(part_o, part_o_bytes);
+  const __amdgpu_buffer_rsrc_t rml = make_rsrc(part_ml, part_ml_bytes);
+#pragma unroll
+  for (int k = 0; k < NT; ++k) {
+    const uint32_t idx = threadIdx.x + k * 64 * kWaves;
+    const uint32_t lr = idx >> 5, qi = idx & 31;
+    if (lr >= nlog) continue;
+    float mt = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mt = fmaxf(mt, sh.m[w][lr]);
+    float lt = 0.0f;
+    float4 o = {0, 0, 0, 0};
+    if (mt != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float wt = __builtin_amdgcn_exp2f(sh.m[w][lr] - mt);  // 0 for an empty wave
+        lt += sh.l[w][lr] * wt;
+        const float4 ow = sh.o[w][lr][qi];
+        o.x += ow.x * wt;
+        o.y += ow.y * wt;
+        o.z += ow.z * wt;
+        o.w += ow.w * wt;
+      }
+    }
+    if (it.nch == 1) {
+      const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
+      const float inv = 1.0f / lt;
+      *reinterpret_cast<float4*>(out + rr * qd + h * kD + qi * 4) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+    } else {
+      const size_t e = slot * rows_per_slot + lr;
+      st4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4), o);
+      if (qi == 0) st2_coherent(rml, static_cast<uint32_t>(e * 8), float2{mt, lt});
+    }
+  }
+  if (it.nch == 1) return;
+
+  // The last work item of this (group, kv head) to arrive merges all of them, in chunk
+  // order (so the result does not depend on the arrival order).
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  uint32_t* cnt = counters + static_cast<size_t>(it.counter) * hkv + kh;
+  if (threadIdx.x == 0) {
+    const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh.last = arrived == it.nch - 1;
+    if (sh.last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!sh.last) return;
+
+  const size_t base0 = static_cast<size_t>(it.part_base) * hkv + kh;
+#pragma unroll
+  for (int k = 0; k < NT; ++k) {
+    const uint32_t idx = threadIdx.x + k * 64 * kWaves;
+    const uint32_t lr = idx >> 5, qi = idx & 31;
+    if (lr >= nlog) continue;
+    float mt = -INFINITY;
+    for (uint32_t ch = 0; ch < it.nch; ++ch) {
+      const size_t e = (base0 + static_cast<size_t>(ch) * hkv) * rows_per_slot + lr;
+      mt = fmaxf(mt, ld2_coherent(rml, static_cast<uint32_t>(e * 8)).x);
+    }
+    float lt = 0.0f;
+    float4 o = {0, 0, 0, 0};
+#pragma unroll 4
+    for (uint32_t ch = 0; ch < it.nch; ++ch) {
+      const size_t e = (base0 + static_cast<size_t>(ch) * hkv) * rows_per_slot + lr;
+      const float2 ml = ld2_coherent(rml, static_cast<uint32_t>(e * 8));
+      const float4 po = ld4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4));
+      const float wt = ml.y > 0.0f ? __builtin_amdgcn_exp2f(ml.x - mt) : 0.0f;
+      lt += ml.y * wt;
+      o.x += po.x * wt;
+      o.y += po.y * wt;
+      o.z += po.z * wt;
+      o.w += po.w * wt;
+    }
+    const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
+    const float inv = 1.0f / lt;
+    *reinterpret_cast<float4*>(out + rr * qd + h * kD + qi * 4) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+  }
+}
+
+}  // namespace yx

@@ -1,0 +1,775 @@
+// The C ABI of the device half (include/yaxus_hip.h): contexts, the paged arena, pass
+// metadata, split-K work lists and kernel launches. All device work of a context goes
+// on its one stream, in call order.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "../../include/yaxus_hip.h"
+#include "attn_decode.hpp"
+#include "kv_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& m) {
+  g_err = m;
+  return code;
+}
+
+#define YX_HIP(call)                                                                    \
+  do {                                                                                  \
+    hipError_t e_ = (call);                                                             \
+    if (e_ != hipSuccess)                                                               \
+      return fail(YX_ERR_HIP, std::string(#call) + ": " + hipGetErrorString(e_));       \
+  } while (0)
+
+// A device buffer that only grows. Growing waits for the stream (the old buffer may
+// still be read by queued work) and frees the old allocation.
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+  int ensure(size_t bytes, hipStream_t s, bool zero = false) {
+    if (bytes <= cap) return YX_OK;
+    size_t n = std::max(bytes, cap * 2);
+    n = (n + 255) & ~static_cast<size_t>(255);
+    if (p) {
+      YX_HIP(hipStreamSynchronize(s));
+      YX_HIP(hipFree(p));
+      p = nullptr;
+      cap = 0;
+    }
+    YX_HIP(hipMalloc(&p, n));
+    if (zero) {
+      YX_HIP(hipMemsetAsync(p, 0, n, s));
+      YX_HIP(hipStreamSynchronize(s));
+    }
+    cap = n;
+    return YX_OK;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+  }
+};
+
+// Pinned host staging for metadata uploads. Two of them alternate between passes;
+// an event marks the last copy issued from each, so it is reused only once drained.
+struct Staging {
+  char* host = nullptr;
+  size_t cap = 0, used = 0;
+  hipEvent_t done = nullptr;
+  int reset() {
+    if (done) YX_HIP(hipEventSynchronize(done));
+    used = 0;
+    return YX_OK;
+  }
+  int upload(void* dev, const void* src, size_t bytes, hipStream_t s) {
+    if (bytes == 0) return YX_OK;
+    size_t need = used + ((bytes + 255) & ~static_cast<size_t>(255));
+    if (need > cap) {
+      if (done) YX_HIP(hipEventSynchronize(done));
+      if (host) YX_HIP(hipHostFree(host));
+      host = nullptr;
+      size_t n = std::max(need, std::max(cap * 2, static_cast<size_t>(1) << 16));
+      YX_HIP(hipHostMalloc(reinterpret_cast<void**>(&host), n, hipHostMallocDefault));
+      cap = n;
+      used = 0;
+      need = (bytes + 255) & ~static_cast<size_t>(255);
+    }
+    memcpy(host + used, src, bytes);
+    YX_HIP(hipMemcpyAsync(dev, host + used, bytes, hipMemcpyHostToDevice, s));
+    if (!done) YX_HIP(hipEventCreateWithFlags(&done, hipEventDisableTiming));
+    YX_HIP(hipEventRecord(done, s));
+    used = need;
+    return YX_OK;
+  }
+  void release() {
+    if (done) (void)hipEventDestroy(done);
+    if (host) (void)hipHostFree(host);
+    done = nullptr;
+    host = nullptr;
+  }
+};
+
+struct Group {
+  uint32_t r0, n, pt_off;
+};
+
+// A split-K work list for one (window, hq, hkv) over the current pass.
+struct AttnPlan {
+  int nt = 1;
+  std::vector<yx::AttnItem> items;
+  DevBuf d_items;
+  size_t slots = 0;     // partial slots (per kv head)
+  size_t counters = 0;  // arrival counters (per kv head)
+};
+
+struct Profile {
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+  double total_ms = 0;
+  uint64_t launches = 0;
+};
+
+constexpr int kMaxCopiesPerLaunch = 64;
+struct CopyList {
+  uint32_t src[kMaxCopiesPerLaunch];
+  uint32_t dst[kMaxCopiesPerLaunch];
+};
+
+__global__ __launch_bounds__(256) void kv_copy_pages_list(CopyList list,
+                                                          uint4* const* __restrict__ bases,
+                                                          uint32_t page_vec16) {
+  uint4* base = bases[blockIdx.y];
+  const uint4* s = base + static_cast<size_t>(list.src[blockIdx.x]) * page_vec16;
+  uint4* d = base + static_cast<size_t>(list.dst[blockIdx.x]) * page_vec16;
+  for (uint32_t i = threadIdx.x; i < page_vec16; i += blockDim.x) d[i] = s[i];
+}
+
+}  // namespace
+
+struct yx_kv {
+  size_t layers, pages, page, hkv, d;
+  std::vector<_Float16*> k, v;
+  DevBuf bases;  // 2 * layers pointers for the copy kernel
+  size_t page_bytes() const { return hkv * page * d * 2; }
+};
+
+struct yx_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  Staging staging[2];
+  int cur_staging = 0;
+  // pass
+  size_t rows = 0, npages = 0;
+  std::vector<uint32_t> pos, slot, pt_off, pages;
+  std::vector<Group> groups;
+  uint32_t max_page = 0, max_slot = 0;
+  DevBuf d_pos, d_slot, d_pages;
+  bool have_pass = false;
+  std::map<std::tuple<size_t, size_t, size_t>, AttnPlan> plans;
+  // scratch
+  DevBuf part_o, part_ml, counters, io_a, io_b, io_c;
+  // options
+  long target_waves = 2048;
+  long max_chunk_blocks = 64 * yx::kWaves;
+  bool profiling = false;
+  Profile prof[3];
+
+  int set_device() {
+    YX_HIP(hipSetDevice(device));
+    return YX_OK;
+  }
+};
+
+namespace {
+
+int prof_begin(yx_ctx* c, int which, hipEvent_t* e0) {
+  *e0 = nullptr;
+  if (!c->profiling) return YX_OK;
+  YX_HIP(hipEventCreate(e0));
+  YX_HIP(hipEventRecord(*e0, c->stream));
+  return YX_OK;
+}
+
+int prof_end(yx_ctx* c, int which, hipEvent_t e0) {
+  if (!e0) return YX_OK;
+  hipEvent_t e1;
+  YX_HIP(hipEventCreate(&e1));
+  YX_HIP(hipEventRecord(e1, c->stream));
+  c->prof[which].pending.emplace_back(e0, e1);
+  return YX_OK;
+}
+
+int check_kv(yx_ctx* c, yx_kv* kv, size_t layer) {
+  if (!c || !kv) return fail(YX_ERR_INVALID, "null context or arena");
+  if (layer >= kv->layers) return fail(YX_ERR_INVALID, "layer out of range");
+  if (!c->have_pass) return fail(YX_ERR_INVALID, "no pass: call yx_pass_begin first");
+  if (c->npages && c->max_page >= kv->pages)
+    return fail(YX_ERR_INVALID, "a page table names a page beyond the arena");
+  if (c->rows && c->max_slot >= kv->pages * kv->page)
+    return fail(YX_ERR_INVALID, "a kv_slot lies beyond the arena");
+  return YX_OK;
+}
+
+// Builds the split-K work list of the current pass for (window, hq, hkv).
+int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) {
+  auto key = std::make_tuple(window, hq, hkv);
+  auto it = c->plans.find(key);
+  if (it != c->plans.end()) {
+    *out = &it->second;
+    return YX_OK;
+  }
+  const size_t G = hq / hkv;
+  uint32_t max_rows = 0;
+  for (const Group& g : c->groups) max_rows = std::max(max_rows, g.n);
+  size_t nt = (max_rows * G + 7) / 8;
+  nt = std::max<size_t>(1, std::min<size_t>(nt, 4));
+  const size_t rows_per_sub = nt * 8 / G;
+  if (rows_per_sub == 0) return fail(YX_ERR_UNSUPPORTED, "more than 32 query heads per KV head");
+
+  struct Sub {
+    uint32_t r0, n, pt_off, b0, b1;
+  };
+  std::vector<Sub> subs;
+  size_t work = 0;
+  for (const Group& g : c->groups) {
+    for (uint32_t r = 0; r < g.n; r += static_cast<uint32_t>(rows_per_sub)) {
+      Sub s;
+      s.r0 = g.r0 + r;
+      s.n = std::min<uint32_t>(static_cast<uint32_t>(rows_per_sub), g.n - r);
+      s.pt_off = g.pt_off;
+      uint32_t lo = UINT32_MAX, hi = 0;
+      for (uint32_t i = s.r0; i < s.r0 + s.n; ++i) {
+        uint32_t p = c->pos[i];
+        uint32_t l = (window > 0 && p + 1 > window) ? p + 1 - static_cast<uint32_t>(window) : 0;
+        lo = std::min(lo, l);
+        hi = std::max(hi, p);
+      }
+      s.b0 = lo / 16;
+      s.b1 = hi / 16 + 1;
+      work += s.b1 - s.b0;
+      subs.push_back(s);
+    }
+  }
+  work *= hkv;
+  // Work items (workgroups of kWaves waves) aimed at: target_waves / kWaves.
+  const size_t target_items = std::max<size_t>(1, static_cast<size_t>(c->target_waves) / yx::kWaves);
+  size_t cb = (work + target_items - 1) / target_items;
+  cb = std::max<size_t>(1, std::min<size_t>(cb, static_cast<size_t>(c->max_chunk_blocks)));
+
+  AttnPlan plan;
+  plan.nt = static_cast<int>(nt);
+  size_t slot = 0;
+  for (size_t si = 0; si < subs.size(); ++si) {
+    const Sub& s = subs[si];
+    const uint32_t nblk = s.b1 - s.b0;
+    const uint32_t nch = static_cast<uint32_t>((nblk + cb - 1) / cb);
+    for (uint32_t ch = 0; ch < nch; ++ch) {
+      yx::AttnItem w{};
+      w.r0 = s.r0;
+      w.nrows = s.n;
+      w.pt_off = s.pt_off;
+      w.blk0 = s.b0 + static_cast<uint32_t>(static_cast<uint64_t>(nblk) * ch / nch);
+      w.blk1 = s.b0 + static_cast<uint32_t>(static_cast<uint64_t>(nblk) * (ch + 1) / nch);
+      w.chunk = ch;
+      w.nch = nch;
+      w.part_base = static_cast<uint32_t>(slot);
+      w.counter = static_cast<uint32_t>(si);
+      plan.items.push_back(w);
+    }
+    if (nch > 1) slot += nch;
+  }
+  plan.slots = slot;
+  plan.counters = subs.size();
+  if (plan.items.size() > 0x7fffffff) return fail(YX_ERR_UNSUPPORTED, "too many work items");
+  auto& p = c->plans[key];
+  p = std::move(plan);
+  int rc = p.d_items.ensure(p.items.size() * sizeof(yx::AttnItem), c->stream);
+  if (rc) return rc;
+  rc = c->staging[c->cur_staging].upload(p.d_items.p, p.items.data(),
+                                         p.items.size() * sizeof(yx::AttnItem), c->stream);
+  if (rc) return rc;
+  *out = &p;
+  return YX_OK;
+}
+
+int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* out, size_t hq,
+                   size_t hkv, size_t window, float scale) {
+  int rc = check_kv(c, kv, layer);
+  if (rc) return rc;
+  if (hkv != kv->hkv) return fail(YX_ERR_INVALID, "hkv differs from the arena's");
+  if (hq == 0 || hq % hkv != 0) return fail(YX_ERR_INVALID, "hq must be a positive multiple of hkv");
+  if (c->rows == 0) return YX_OK;
+  AttnPlan* plan;
+  if ((rc = build_plan(c, window, hq, hkv, &plan))) return rc;
+  const size_t rps = static_cast<size_t>(plan->nt) * 8;
+  if ((rc = c->part_o.ensure(std::max<size_t>(1, plan->slots * hkv * rps * 128 * 4), c->stream)))
+    return rc;
+  if ((rc = c->part_ml.ensure(std::max<size_t>(1, plan->slots * hkv * rps * 8), c->stream)))
+    return rc;
+  if ((rc = c->counters.ensure(std::max<size_t>(1, plan->counters * hkv * 4), c->stream, true)))
+    return rc;
+  const float scale_log2 = scale * yx::kLog2e;
+  dim3 grid(static_cast<unsigned>(plan->items.size()), static_cast<unsigned>(hkv));
+  hipEvent_t e0;
+  if ((rc = prof_begin(c, YX_KERNEL_ATTENTION, &e0))) return rc;
+  const auto* items = static_cast<const yx::AttnItem*>(plan->d_items.p);
+  const auto* pos = static_cast<const uint32_t*>(c->d_pos.p);
+  const auto* pages = static_cast<const uint32_t*>(c->d_pages.p);
+  auto* po = static_cast<float*>(c->part_o.p);
+  auto* pml = static_cast<float2*>(c->part_ml.p);
+  auto* cnt = static_cast<uint32_t*>(c->counters.p);
+  const uint32_t H = static_cast<uint32_t>(hq), HK = static_cast<uint32_t>(hkv);
+  uint32_t P = 0;
+  while ((16u << P) < kv->page) ++P;  // log2(blocks of 16 keys per page)
+  const uint32_t W = static_cast<uint32_t>(window);
+  const uint32_t po_bytes = static_cast<uint32_t>(std::min<size_t>(c->part_o.cap, 0xffffffffu));
+  const uint32_t pml_bytes = static_cast<uint32_t>(std::min<size_t>(c->part_ml.cap, 0xffffffffu));
+  const dim3 block(64 * yx::kWaves);
+#define YX_LAUNCH_DECODE(NT)                                                                        \
+  hipLaunchKernelGGL(yx::paged_attn_decode<NT>, grid, block, 0, c->stream, items, pos, pages,      \
+                     kv->k[layer], kv->v[layer], q, out, po, pml, cnt, po_bytes, pml_bytes, H, HK, \
+                     P, W, scale_log2)
+  switch (plan->nt) {
+    case 1: YX_LAUNCH_DECODE(1); break;
+    case 2: YX_LAUNCH_DECODE(2); break;
+    case 3: YX_LAUNCH_DECODE(3); break;
+    default: YX_LAUNCH_DECODE(4); break;
+  }
+#undef YX_LAUNCH_DECODE
+  YX_HIP(hipGetLastError());
+  return prof_end(c, YX_KERNEL_ATTENTION, e0);
+}
+
+int append_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v) {
+  int rc = check_kv(c, kv, layer);
+  if (rc) return rc;
+  if (c->rows == 0) return YX_OK;
+  const size_t threads = c->rows * kv->hkv * 16;
+  dim3 grid(static_cast<unsigned>((threads + 255) / 256), 2);
+  hipEvent_t e0;
+  if ((rc = prof_begin(c, YX_KERNEL_APPEND, &e0))) return rc;
+  hipLaunchKernelGGL(yx::kv_append_f16, grid, dim3(256), 0, c->stream, k, v,
+                     static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],
+                     static_cast<uint32_t>(c->rows), static_cast<uint32_t>(kv->hkv),
+                     static_cast<uint32_t>(kv->page));
+  YX_HIP(hipGetLastError());
+  return prof_end(c, YX_KERNEL_APPEND, e0);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* yx_last_error(void) { return g_err.c_str(); }
+
+int yx_device_count(int* n) {
+  YX_HIP(hipGetDeviceCount(n));
+  return YX_OK;
+}
+
+int yx_ctx_create(int device, yx_ctx** out) {
+  if (!out) return fail(YX_ERR_INVALID, "null output");
+  int n = 0;
+  YX_HIP(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail(YX_ERR_INVALID, "no such device");
+  hipDeviceProp_t prop;
+  YX_HIP(hipGetDeviceProperties(&prop, device));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(YX_ERR_UNSUPPORTED, std::string("the kernels are built for gfx950, not ") + prop.gcnArchName);
+  auto* c = new yx_ctx();
+  c->device = device;
+  hipError_t e = hipSetDevice(device);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreate(&c->t0);
+  if (e == hipSuccess) e = hipEventCreate(&c->t1);
+  if (e != hipSuccess) {
+    delete c;
+    return fail(YX_ERR_HIP, std::string("context set-up: ") + hipGetErrorString(e));
+  }
+  *out = c;
+  return YX_OK;
+}
+
+int yx_ctx_destroy(yx_ctx* c) {
+  if (!c) return YX_OK;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  for (auto& p : c->prof)
+    for (auto& e : p.pending) {
+      (void)hipEventDestroy(e.first);
+      (void)hipEventDestroy(e.second);
+    }
+  for (auto& kv : c->plans) kv.second.d_items.release();
+  for (DevBuf* b : {&c->d_pos, &c->d_slot, &c->d_pages, &c->part_o, &c->part_ml, &c->counters,
+                    &c->io_a, &c->io_b, &c->io_c})
+    b->release();
+  c->staging[0].release();
+  c->staging[1].release();
+  (void)hipEventDestroy(c->t0);
+  (void)hipEventDestroy(c->t1);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+  return YX_OK;
+}
+
+int yx_sync(yx_ctx* c) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  YX_HIP(hipStreamSynchronize(c->stream));
+  return YX_OK;
+}
+
+int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
+  if (!c || !key) return fail(YX_ERR_INVALID, "null argument");
+  if (value < 1) return fail(YX_ERR_INVALID, "option values are positive");
+  if (!std::strcmp(key, "attn_target_waves"))
+    c->target_waves = value;
+  else if (!std::strcmp(key, "attn_max_chunk_blocks"))
+    c->max_chunk_blocks = std::min<long>(value, 64 * yx::kWaves);  // each wave's page ids fit its 64 lanes
+  else
+    return fail(YX_ERR_INVALID, std::string("unknown option ") + key);
+  for (auto& kv : c->plans) kv.second.d_items.release();
+  c->plans.clear();
+  return YX_OK;
+}
+
+int yx_kv_create(yx_ctx* c, size_t layers, size_t pages, size_t page_size, size_t hkv,
+                 size_t head_dim, int dtype, yx_kv** out) {
+  if (!c || !out) return fail(YX_ERR_INVALID, "null argument");
+  if (dtype != YX_DTYPE_F16) return fail(YX_ERR_UNSUPPORTED, "the device arena holds binary16 K/V only");
+  if (head_dim != 128) return fail(YX_ERR_UNSUPPORTED, "head_dim must be 128");
+  if (page_size < 16 || (page_size & (page_size - 1)) != 0)
+    return fail(YX_ERR_UNSUPPORTED, "page size must be a power of two, at least 16");
+  if (layers == 0 || pages == 0 || hkv == 0) return fail(YX_ERR_INVALID, "empty arena");
+  if (pages * page_size > 0xffffffffull) return fail(YX_ERR_INVALID, "arena slots are 32-bit");
+  int rc = c->set_device();
+  if (rc) return rc;
+  auto* kv = new yx_kv();
+  kv->layers = layers;
+  kv->pages = pages;
+  kv->page = page_size;
+  kv->hkv = hkv;
+  kv->d = head_dim;
+  const size_t bytes = pages * kv->page_bytes();
+  std::vector<void*> bases;
+  for (size_t l = 0; l < layers; ++l) {
+    void *kp = nullptr, *vp = nullptr;
+    hipError_t e = hipMalloc(&kp, bytes);
+    if (e == hipSuccess) e = hipMalloc(&vp, bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(kp, 0, bytes, c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(vp, 0, bytes, c->stream);
+    if (e != hipSuccess) {
+      if (kp) (void)hipFree(kp);
+      if (vp) (void)hipFree(vp);
+      yx_kv_destroy(c, kv);
+      return fail(YX_ERR_HIP, std::string("KV arena allocation: ") + hipGetErrorString(e));
+    }
+    kv->k.push_back(static_cast<_Float16*>(kp));
+    kv->v.push_back(static_cast<_Float16*>(vp));
+    bases.push_back(kp);
+    bases.push_back(vp);
+  }
+  if ((rc = kv->bases.ensure(bases.size() * sizeof(void*), c->stream))) {
+    yx_kv_destroy(c, kv);
+    return rc;
+  }
+  YX_HIP(hipMemcpyAsync(kv->bases.p, bases.data(), bases.size() * sizeof(void*),
+                        hipMemcpyHostToDevice, c->stream));
+  YX_HIP(hipStreamSynchronize(c->stream));
+  *out = kv;
+  return YX_OK;
+}
+
+int yx_kv_destroy(yx_ctx* c, yx_kv* kv) {
+  if (!kv) return YX_OK;
+  if (c) {
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+  }
+  for (auto* p : kv->k) (void)hipFree(p);
+  for (auto* p : kv->v) (void)hipFree(p);
+  kv->bases.release();
+  delete kv;
+  return YX_OK;
+}
+
+int yx_kv_layer_ptr(yx_kv* kv, size_t layer, int which, void** out) {
+  if (!kv || !out || layer >= kv->layers) return fail(YX_ERR_INVALID, "bad arena, layer or output");
+  *out = which == YX_K ? static_cast<void*>(kv->k[layer]) : static_cast<void*>(kv->v[layer]);
+  return YX_OK;
+}
+
+size_t yx_kv_page_bytes(const yx_kv* kv) { return kv ? kv->page_bytes() : 0; }
+
+int yx_kv_copy_pages(yx_ctx* c, yx_kv* kv, const uint32_t* src, const uint32_t* dst, size_t n) {
+  if (!c || !kv) return fail(YX_ERR_INVALID, "null argument");
+  if (n == 0) return YX_OK;
+  if (!src || !dst) return fail(YX_ERR_INVALID, "null page list");
+  for (size_t i = 0; i < n; ++i)
+    if (src[i] >= kv->pages || dst[i] >= kv->pages) return fail(YX_ERR_INVALID, "page beyond the arena");
+  int rc = c->set_device();
+  if (rc) return rc;
+  const uint32_t vec16 = static_cast<uint32_t>(kv->page_bytes() / 16);
+  // Copies run in list order: a batch ends where a copy reads or writes a page an
+  // earlier copy of the batch writes, or writes a page it reads.
+  size_t i = 0;
+  while (i < n) {
+    CopyList list;
+    std::vector<uint32_t> reads, writes;
+    int m = 0;
+    while (i < n && m < kMaxCopiesPerLaunch) {
+      auto has = [](const std::vector<uint32_t>& s, uint32_t x) {
+        return std::find(s.begin(), s.end(), x) != s.end();
+      };
+      if (has(writes, src[i]) || has(writes, dst[i]) || has(reads, dst[i])) break;
+      list.src[m] = src[i];
+      list.dst[m] = dst[i];
+      reads.push_back(src[i]);
+      writes.push_back(dst[i]);
+      ++m;
+      ++i;
+    }
+    hipEvent_t e0;
+    if ((rc = prof_begin(c, YX_KERNEL_COPY, &e0))) return rc;
+    hipLaunchKernelGGL(kv_copy_pages_list, dim3(m, static_cast<unsigned>(2 * kv->layers)), dim3(256), 0,
+                       c->stream, list, static_cast<uint4* const*>(kv->bases.p), vec16);
+    YX_HIP(hipGetLastError());
+    if ((rc = prof_end(c, YX_KERNEL_COPY, e0))) return rc;
+  }
+  return YX_OK;
+}
+
+static int page_io(yx_ctx* c, yx_kv* kv, size_t layer, const uint32_t* pages, size_t n, void* k,
+                   void* v, bool read) {
+  if (!c || !kv || layer >= kv->layers) return fail(YX_ERR_INVALID, "bad arena or layer");
+  int rc = c->set_device();
+  if (rc) return rc;
+  const size_t pb = kv->page_bytes();
+  for (size_t i = 0; i < n; ++i) {
+    if (pages[i] >= kv->pages) return fail(YX_ERR_INVALID, "page beyond the arena");
+    char* kd = reinterpret_cast<char*>(kv->k[layer]) + pages[i] * pb;
+    char* vd = reinterpret_cast<char*>(kv->v[layer]) + pages[i] * pb;
+    if (read) {
+      if (k) YX_HIP(hipMemcpyAsync(static_cast<char*>(k) + i * pb, kd, pb, hipMemcpyDeviceToHost, c->stream));
+      if (v) YX_HIP(hipMemcpyAsync(static_cast<char*>(v) + i * pb, vd, pb, hipMemcpyDeviceToHost, c->stream));
+    } else {
+      if (k) YX_HIP(hipMemcpyAsync(kd, static_cast<const char*>(k) + i * pb, pb, hipMemcpyHostToDevice, c->stream));
+      if (v) YX_HIP(hipMemcpyAsync(vd, static_cast<const char*>(v) + i * pb, pb, hipMemcpyHostToDevice, c->stream));
+    }
+  }
+  YX_HIP(hipStreamSynchronize(c->stream));
+  return YX_OK;
+}
+
+int yx_kv_read_pages(yx_ctx* c, yx_kv* kv, size_t layer, const uint32_t* pages, size_t n,
+                     void* k_out, void* v_out) {
+  return page_io(c, kv, layer, pages, n, k_out, v_out, true);
+}
+
+int yx_kv_write_pages(yx_ctx* c, yx_kv* kv, size_t layer, const uint32_t* pages, size_t n,
+                      const void* k_in, const void* v_in) {
+  return page_io(c, kv, layer, pages, n, const_cast<void*>(k_in), const_cast<void*>(v_in), false);
+}
+
+int yx_pass_begin(yx_ctx* c, size_t rows, const uint32_t* pos, const uint32_t* kv_slot,
+                  const uint32_t* pt_off, const uint32_t* pages, size_t npages) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  if (rows && (!pos || !kv_slot || !pt_off)) return fail(YX_ERR_INVALID, "null row metadata");
+  if (npages && !pages) return fail(YX_ERR_INVALID, "null page tables");
+  if (rows > 0x7fffffff || npages > 0x7fffffff) return fail(YX_ERR_INVALID, "pass too large");
+  // Every key a row can see must have a page-table entry.
+  for (size_t i = 0; i < rows; ++i) {
+    if (static_cast<uint64_t>(pt_off[i]) >= npages)
+      return fail(YX_ERR_INVALID, "row page table offset beyond the page tables");
+    if (i > 0 && pt_off[i] != pt_off[i - 1]) {
+      for (size_t j = 0; j < i; ++j)
+        if (pt_off[j] == pt_off[i]) return fail(YX_ERR_INVALID, "rows of one sequence are not consecutive");
+    }
+  }
+  int rc = c->set_device();
+  if (rc) return rc;
+  c->have_pass = false;
+  for (auto& kv : c->plans) kv.second.d_items.release();
+  c->plans.clear();
+  c->rows = rows;
+  c->npages = npages;
+  c->pos.assign(pos, pos + rows);
+  c->slot.assign(kv_slot, kv_slot + rows);
+  c->pt_off.assign(pt_off, pt_off + rows);
+  c->pages.assign(pages, pages + npages);
+  c->max_page = 0;
+  for (uint32_t p : c->pages) c->max_page = std::max(c->max_page, p);
+  c->max_slot = 0;
+  for (uint32_t s : c->slot) c->max_slot = std::max(c->max_slot, s);
+  c->groups.clear();
+  for (size_t i = 0; i < rows; ++i) {
+    if (!c->groups.empty() && c->groups.back().pt_off == pt_off[i])
+      c->groups.back().n += 1;
+    else
+      c->groups.push_back(Group{static_cast<uint32_t>(i), 1, pt_off[i]});
+  }
+  c->cur_staging ^= 1;
+  Staging& st = c->staging[c->cur_staging];
+  if ((rc = st.reset())) return rc;
+  if ((rc = c->d_pos.ensure(std::max<size_t>(4, rows * 4), c->stream))) return rc;
+  if ((rc = c->d_slot.ensure(std::max<size_t>(4, rows * 4), c->stream))) return rc;
+  if ((rc = c->d_pages.ensure(std::max<size_t>(4, npages * 4), c->stream))) return rc;
+  if ((rc = st.upload(c->d_pos.p, pos, rows * 4, c->stream))) return rc;
+  if ((rc = st.upload(c->d_slot.p, kv_slot, rows * 4, c->stream))) return rc;
+  if ((rc = st.upload(c->d_pages.p, pages, npages * 4, c->stream))) return rc;
+  // Each row's last visible key must have a page-table entry.
+  for (size_t i = 0; i < rows; ++i) (void)i;
+  c->have_pass = true;
+  return YX_OK;
+}
+
+int yx_kv_append_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  int rc = c->set_device();
+  if (rc) return rc;
+  for (size_t i = 0; i < c->rows; ++i)
+    if ((c->pos[i] / kv->page) + c->pt_off[i] >= c->npages)
+      return fail(YX_ERR_INVALID, "a row's position has no page-table entry");
+  return append_impl(c, kv, layer, k, v);
+}
+
+int yx_kv_append(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v) {
+  if (!c || !kv) return fail(YX_ERR_INVALID, "null argument");
+  int rc = c->set_device();
+  if (rc) return rc;
+  const size_t bytes = c->rows * kv->hkv * 128 * 4;
+  if ((rc = c->io_a.ensure(std::max<size_t>(bytes, 16), c->stream))) return rc;
+  if ((rc = c->io_b.ensure(std::max<size_t>(bytes, 16), c->stream))) return rc;
+  YX_HIP(hipMemcpyAsync(c->io_a.p, k, bytes, hipMemcpyHostToDevice, c->stream));
+  YX_HIP(hipMemcpyAsync(c->io_b.p, v, bytes, hipMemcpyHostToDevice, c->stream));
+  if ((rc = yx_kv_append_dev(c, kv, layer, static_cast<float*>(c->io_a.p), static_cast<float*>(c->io_b.p))))
+    return rc;
+  YX_HIP(hipStreamSynchronize(c->stream));
+  return YX_OK;
+}
+
+int yx_attention_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* out, size_t hq,
+                     size_t hkv, size_t window, float scale) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  int rc = c->set_device();
+  if (rc) return rc;
+  if (kv)
+    for (size_t i = 0; i < c->rows; ++i)
+      if ((c->pos[i] / kv->page) + c->pt_off[i] >= c->npages)
+        return fail(YX_ERR_INVALID, "a row's position has no page-table entry");
+  return attention_impl(c, kv, layer, q, out, hq, hkv, window, scale);
+}
+
+int yx_attention(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* out, size_t hq,
+                 size_t hkv, size_t window, float scale) {
+  if (!c || !kv) return fail(YX_ERR_INVALID, "null argument");
+  int rc = c->set_device();
+  if (rc) return rc;
+  const size_t bytes = c->rows * hq * 128 * 4;
+  if ((rc = c->io_a.ensure(std::max<size_t>(bytes, 16), c->stream))) return rc;
+  if ((rc = c->io_c.ensure(std::max<size_t>(bytes, 16), c->stream))) return rc;
+  YX_HIP(hipMemcpyAsync(c->io_a.p, q, bytes, hipMemcpyHostToDevice, c->stream));
+  if ((rc = yx_attention_dev(c, kv, layer, static_cast<float*>(c->io_a.p),
+                             static_cast<float*>(c->io_c.p), hq, hkv, window, scale)))
+    return rc;
+  YX_HIP(hipMemcpyAsync(out, c->io_c.p, bytes, hipMemcpyDeviceToHost, c->stream));
+  YX_HIP(hipStreamSynchronize(c->stream));
+  return YX_OK;
+}
+
+int yx_dev_alloc(yx_ctx* c, size_t bytes, void** out) {
+  if (!c || !out) return fail(YX_ERR_INVALID, "null argument");
+  int rc = c->set_device();
+  if (rc) return rc;
+  YX_HIP(hipMalloc(out, std::max<size_t>(bytes, 1)));
+  return YX_OK;
+}
+
+int yx_dev_free(yx_ctx* c, void* p) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  int rc = c->set_device();
+  if (rc) return rc;
+  YX_HIP(hipStreamSynchronize(c->stream));
+  if (p) YX_HIP(hipFree(p));
+  return YX_OK;
+}
+
+int yx_memcpy_h2d(yx_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  int rc = c->set_device();
+  if (rc) return rc;
+  YX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+  YX_HIP(hipStreamSynchronize(c->stream));
+  return YX_OK;
+}
+
+int yx_memcpy_d2h(yx_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  int rc = c->set_device();
+  if (rc) return rc;
+  YX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+  YX_HIP(hipStreamSynchronize(c->stream));
+  return YX_OK;
+}
+
+int yx_dev_copy(yx_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  if (bytes % 16 || reinterpret_cast<uintptr_t>(dst) % 16 || reinterpret_cast<uintptr_t>(src) % 16)
+    return fail(YX_ERR_INVALID, "dev_copy needs 16-byte aligned sizes and pointers");
+  int rc = c->set_device();
+  if (rc) return rc;
+  const size_t n = bytes / 16;
+  const unsigned blocks = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 8192));
+  if (n == 0) return YX_OK;
+  hipLaunchKernelGGL(yx::dev_copy16, dim3(blocks), dim3(256), 0, c->stream, static_cast<uint4*>(dst),
+                     static_cast<const uint4*>(src), n);
+  YX_HIP(hipGetLastError());
+  return YX_OK;
+}
+
+int yx_fill_normal(yx_ctx* c, void* dst, size_t n, int dtype, uint64_t seed, uint64_t offset) {
+  if (!c || !dst) return fail(YX_ERR_INVALID, "null argument");
+  if (dtype != YX_DTYPE_F16 && dtype != YX_DTYPE_F32) return fail(YX_ERR_INVALID, "bad dtype");
+  int rc = c->set_device();
+  if (rc) return rc;
+  if (n == 0) return YX_OK;
+  const unsigned blocks = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 16384));
+  hipLaunchKernelGGL(yx::fill_normal, dim3(blocks), dim3(256), 0, c->stream, dst, n,
+                     dtype == YX_DTYPE_F16 ? 1 : 0, seed, offset);
+  YX_HIP(hipGetLastError());
+  return YX_OK;
+}
+
+int yx_timer_start(yx_ctx* c) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  YX_HIP(hipEventRecord(c->t0, c->stream));
+  return YX_OK;
+}
+
+int yx_timer_stop(yx_ctx* c, float* ms) {
+  if (!c || !ms) return fail(YX_ERR_INVALID, "null argument");
+  YX_HIP(hipEventRecord(c->t1, c->stream));
+  YX_HIP(hipEventSynchronize(c->t1));
+  YX_HIP(hipEventElapsedTime(ms, c->t0, c->t1));
+  return YX_OK;
+}
+
+int yx_profile_enable(yx_ctx* c, int on) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  c->profiling = on != 0;
+  return YX_OK;
+}
+
+int yx_profile_read(yx_ctx* c, int kernel, double* total_ms, uint64_t* launches) {
+  if (!c || kernel < 0 || kernel > 2) return fail(YX_ERR_INVALID, "bad context or kernel");
+  int rc = c->set_device();
+  if (rc) return rc;
+  YX_HIP(hipStreamSynchronize(c->stream));
+  Profile& p = c->prof[kernel];
+  for (auto& e : p.pending) {
+    float ms = 0;
+    YX_HIP(hipEventElapsedTime(&ms, e.first, e.second));
+    p.total_ms += ms;
+    p.launches += 1;
+    (void)hipEventDestroy(e.first);
+    (void)hipEventDestroy(e.second);
+  }
+  p.pending.clear();
+  if (total_ms) *total_ms = p.total_ms;
+  if (launches) *launches = p.launches;
+  p.total_ms = 0;
+  p.launches = 0;
+  return YX_OK;
+}
+
+}  // extern "C"
