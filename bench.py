@@ -146,8 +146,7 @@ def main():
 
     def step():
         for l in range(LAYERS):
-            hip.append(kv, l, ks[l], vs[l])
-            hip.attend(kv, l, qs[l], HQ, out=outs[l])
+            hip.attend_append(kv, l, ks[l], vs[l], qs[l], HQ, out=outs[l])
 
     for _ in range(args.warmup):
         step()
@@ -190,7 +189,7 @@ def main():
         "data": "synthetic (splitmix64/Box-Muller N(0,1), seed 0x59415855)",
         "config": {
             "workload": "batched paged decode: B=16, ctx 4096, 16q/4kv heads, d 128, "
-                        "f16 KV, page 16, 24 layers (append + attention per layer)",
+                        "f16 KV, page 16, 24 layers (append + attention per layer, one launch)",
             "B": B, "ctx": CTX, "hq": HQ, "hkv": HKV, "head_dim": D, "page": PAGE,
             "layers": LAYERS, "pool_pages": POOL, "bytes_per_layer_step": LAYER_STEP_BYTES,
         },

@@ -91,6 +91,16 @@ int yx_attention(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* q, float* ou
 int yx_attention_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* q, float* out,
                      size_t hq, size_t hkv, size_t window, float scale);
 
+/* Backend::attention's KV half in one launch (lib.rs:132; backend-cpu lib.rs:516-530):
+ * stores the rows' k, v (`[rows][hkv][128]` f32, as yx_kv_append) and then attends
+ * as yx_attention, the rows seeing their own and earlier rows' new keys. */
+int yx_attention_append(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k, const float* v,
+                        const float* q, float* out, size_t hq, size_t hkv, size_t window,
+                        float scale);
+int yx_attention_append_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k,
+                            const float* v, const float* q, float* out, size_t hq, size_t hkv,
+                            size_t window, float scale);
+
 /* Device memory and copies on the context's stream (h2d/d2h are synchronous). */
 int yx_dev_alloc(yx_ctx* ctx, size_t bytes, void** out);
 int yx_dev_free(yx_ctx* ctx, void* p);

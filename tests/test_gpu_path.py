@@ -129,3 +129,24 @@ def test_attention_close_to_f64(hip):
     got = hip.attend(sc.kv, 0, q, hq)
     exact = sc.orc[0].attend_f64(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
     assert np.abs(got - exact).max() < 2e-5
+
+
+@pytest.mark.parametrize("hq,hkv,k,window", [(16, 4, 1, 0), (16, 4, 5, 0), (16, 4, 6, 50),
+                                             (32, 1, 2, 0), (8, 2, 3, 0)])
+def test_fused_append_attention(hip, hq, hkv, k, window):
+    """One launch stores the rows' K/V and attends (the append falls back to its own
+    kernel when a sequence's rows do not fit one work item: hq=32, hkv=1, k=2)."""
+    sc = Scenario(hip, pages=200, page=16, hkv=hkv, pool_seed=4)
+    seqs = [sc.cache.new_seq() for _ in range(5)]
+    sc.prefill(dict(zip(seqs, [0 + 1, 64, 300, 1023, 15])))
+    pr = sc.run_pass([(s, k) for s in seqs])
+    rows = len(pr.meta.pos)
+    kk = sc.draw(rows * hkv * D).reshape(rows, hkv, D)
+    vv = sc.draw(rows * hkv * D).reshape(rows, hkv, D)
+    q = sc.draw(rows * hq * D).reshape(rows, hq * D)
+    got = hip.attend_append(sc.kv, 0, kk, vv, q, hq, window=window)
+    sc.orc[0].store(pr.meta.kv_slot, kk.reshape(rows, -1), vv.reshape(rows, -1))
+    want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
+    assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
+    used = sorted(set(int(p) for s in seqs for p in sc.cache.seq_pages(s)))
+    _check_pages(sc, 0, used)

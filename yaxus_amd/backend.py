@@ -176,6 +176,28 @@ class HipBackend:
                                       scale))
         return o
 
+    # Backend::attention's KV half (lib.rs:132): store the rows' K/V, then attend, in
+    # one launch where the plan allows it.
+    def attend_append(self, kv, layer, k, v, q, hq, window=None, scale=None, out=None):
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(kv.d))) if scale is None else scale
+        w = int(window or 0)
+        if isinstance(q, DeviceTensor):
+            out = out if out is not None else self.tensor((self.rows, hq * kv.d))
+            check_hip(self.L.yx_attention_append_dev(self.ctx, kv.h, layer, k.ptr, v.ptr, q.ptr,
+                                                     out.ptr, hq, kv.hkv, w, scale))
+            return out
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        q = np.ascontiguousarray(q, np.float32)
+        if k.size != self.rows * kv.hkv * kv.d or v.size != k.size:
+            raise ValueError("k/v must be [rows][hkv][head_dim] f32")
+        if q.size != self.rows * hq * kv.d:
+            raise ValueError("q must be [rows][hq][head_dim] f32")
+        o = np.empty((self.rows, hq * kv.d), np.float32)
+        check_hip(self.L.yx_attention_append(self.ctx, kv.h, layer, ptr(k), ptr(v), ptr(q), ptr(o),
+                                             hq, kv.hkv, w, scale))
+        return o
+
     def fill_normal(self, dev_ptr, n, f16, seed, offset=0):
         check_hip(self.L.yx_fill_normal(self.ctx, dev_ptr, n,
                                         _lib.YX_DTYPE_F16 if f16 else _lib.YX_DTYPE_F32,

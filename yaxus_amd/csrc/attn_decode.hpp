@@ -5,31 +5,38 @@
 // through its page table, softmax of q.k * scale, and the weighted sum of V. The
 // reference GPU splits keys into chunks and merges them afterwards (ATTN_SPLIT +
 // ATTN_COMBINE, crates/yaxus-backend-gpu/src/shaders.rs:1466-1637); here too, but the
-// merge is done by the last work item of a (rows, kv head) to finish, in chunk order.
+// merge runs in the same kernel: the last work item of a (rows, kv head) to finish
+// merges all chunks, in chunk order, so results do not depend on arrival order.
 //
-// One workgroup of 4 waves per work item = (a group of consecutive rows of one
-// sequence, one KV head, one chunk of 16-key blocks); its waves split the chunk's
-// blocks and merge through LDS. The group's (row, query head) pairs are "logical rows";
-// NT tiles of 8 logical rows each are kept in MFMA columns as an f16 hi part
-// (columns 0-7) and an f16 lo part (columns 8-15) of q, so q.k is accurate to ~2^-22
-// relative with f16 K exact and f32 accumulation. Per block of 16 keys:
-//   S^T[key][col] = K[key][:] . Q[col][:]   4 x v_mfma_f32_16x16x32_f16
+// Work item = (a group of consecutive rows of one sequence, one KV head, one chunk of
+// 16-key blocks), one workgroup of W waves; the waves split the chunk's blocks and
+// merge through LDS. The group's (row, query head) pairs are "logical rows"; NT tiles
+// of 8 logical rows each sit in MFMA columns as an f16 hi part (columns 0-7) and an
+// f16 lo part (columns 8-15) of q, so q.k keeps ~2^-22 relative accuracy with f16 K
+// exact and f32 accumulation. Per block of 16 keys:
+//   S^T[key][col] = K[key][:] . Q[col][:]         4 x v_mfma_f32_16x16x32_f16
 //   online softmax per column; P = exp2(S*scale*log2e - m) split into hi/lo f16
-//   O^T[dim][col] += V^T[dim][key] P^T[key][col]   8 x v_mfma_f32_16x16x16_f16
-// K is the A operand with lane l holding key l%16, dims p*32 + (l/16)*8 + 0..7 for
-// MFMA p: each lane's 16-byte load reads 16 consecutive bytes of one key row. V is the
-// A operand of the PV product with lane l holding dims (l%16)*8 + j for 4 keys, so
-// each V load is a row-contiguous 16 bytes too and the output lands as 32 consecutive
-// dims of one column per lane.
+//   O^T[dim][col] += V^T[dim][key] P^T[key][col]  8 x v_mfma_f32_16x16x16_f16
+// Operand layouts (lane l, c = l % 16, g = l / 16):
+//   K: A operand of QK, lane holds key c, dims p*32 + g*8 + 0..7 for MFMA p. The arena
+//      stores each 16-key block of K as [p][key][32 dims] (see kv_kernels.hpp), so the
+//      64 lanes' 16-byte loads of one MFMA read 1 KiB contiguous.
+//   V: A operand of PV, lane holds dims c*8 + j of keys 4g..4g+3; V rows are stored
+//      plainly ([key][128 dims]), so each of the 4 loads reads 4 rows contiguous.
+//   The PV output lands as 32 consecutive dims (32g..32g+31) of column c per lane.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "kv_kernels.hpp"
 
 namespace yx {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // One split-K work item (host-built, see runtime.hip).
 struct AttnItem {
@@ -39,7 +46,7 @@ struct AttnItem {
   uint32_t blk0;       // first 16-key block (absolute key / 16) of this chunk
   uint32_t blk1;       // one past the last block of this chunk
   uint32_t chunk;      // chunk index within the group
-  uint32_t nch;        // chunks of the group
+  uint32_t nch;        // chunks of the group (at most kMaxChunks)
   uint32_t part_base;  // first partial slot of the group
   uint32_t counter;    // arrival counter index of the group
   uint32_t pad[3];
@@ -47,6 +54,7 @@ struct AttnItem {
 
 static constexpr float kLog2e = 1.4426950408889634f;
 static constexpr int kD = 128;
+static constexpr uint32_t kMaxChunks = 64;
 
 // Lane l reads lane l^8 (DPP row rotate by 8 within each row of 16 lanes).
 __device__ __forceinline__ float xor8(float x) {
@@ -57,28 +65,10 @@ __device__ __forceinline__ float xor16(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
 }
 
-// K/V of one 16-key block held by a lane (see the header comment for the mapping).
-struct BlockRegs {
-  half8 k[4];
-  half8 v[4];
-};
-
-__device__ __forceinline__ void load_block(BlockRegs& r, const _Float16* __restrict__ kbase,
-                                           const _Float16* __restrict__ vbase, int lane) {
-  const int c = lane & 15, g = lane >> 4;
-  const half8* kp = reinterpret_cast<const half8*>(kbase + c * kD + g * 8);
-#pragma unroll
-  for (int p = 0; p < 4; ++p) r.k[p] = __builtin_nontemporal_load(kp + p * 4);
-  const half8* vp = reinterpret_cast<const half8*>(vbase + (4 * g) * kD + c * 8);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r.v[i] = __builtin_nontemporal_load(vp + i * (kD / 8));
-}
-
 // Write-through 16-byte store / coherent load of split-K partials through a buffer
 // resource with the sc1 cache policy: the data goes to (and comes from) the memory
 // all XCDs share, so the hand-off between workgroups needs no L2 write-back.
 static constexpr int kCoherent = 16;  // sc1
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(p, 0, static_cast<int>(bytes), 0x00020000);
@@ -90,33 +80,59 @@ __device__ __forceinline__ float4 ld4_coherent(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, kCoherent));
 }
 __device__ __forceinline__ void st2_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, float2 v) {
-  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(uint32_t __attribute__((ext_vector_type(2))), v), r,
-                                        static_cast<int>(off), 0, kCoherent);
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, static_cast<int>(off), 0, kCoherent);
 }
 __device__ __forceinline__ float2 ld2_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, kCoherent));
 }
 
-// Waves per workgroup: they share one work item's blocks and merge through LDS.
-static constexpr int kWaves = 4;
+// K/V of one 16-key block held by a lane (see the header comment for the mapping).
+struct BlockRegs {
+  half8 k[4];
+  half8 v[4];
+};
 
+// kblk / vblk: the block's first half in the arena (2048 halves per block and head).
+__device__ __forceinline__ void load_block(BlockRegs& r, const _Float16* __restrict__ kblk,
+                                           const _Float16* __restrict__ vblk, int lane) {
+  const int c = lane & 15, g = lane >> 4;
+  const half8* kp = reinterpret_cast<const half8*>(kblk) + c * 4 + g;  // [p][key c][g]
+#pragma unroll
+  for (int p = 0; p < 4; ++p) r.k[p] = __builtin_nontemporal_load(kp + p * 64);
+  const half8* vp = reinterpret_cast<const half8*>(vblk + (4 * g) * kD + c * 8);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.v[i] = __builtin_nontemporal_load(vp + i * (kD / 8));
+}
+
+// Waves per workgroup (W): they share one work item's blocks and merge through LDS.
+// Eight keep twice the loads in flight per CU that four do at this register use; the
+// LDS of the merge limits NT > 2 to four.
 template <int NT>
+struct DecodeWaves {
+  static constexpr int value = NT <= 2 ? 8 : 4;
+};
+
+template <int NT, int W>
 struct DecodeShared {
-  float m[kWaves][NT * 8];
-  float l[kWaves][NT * 8];
-  float4 o[kWaves][NT * 8][kD / 4];
+  float m[W][NT * 8];
+  float l[W][NT * 8];
+  float4 o[W][NT * 8][kD / 4];  // also holds the (m, l) of all chunks in the final merge
   uint32_t last;
 };
 
-template <int NT>
+template <int NT, int kWaves = DecodeWaves<NT>::value>
 __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
     const AttnItem* __restrict__ items, const uint32_t* __restrict__ pos,
-    const uint32_t* __restrict__ pages, const _Float16* __restrict__ kc,
-    const _Float16* __restrict__ vc, const float* __restrict__ q, float* __restrict__ out,
+    const uint32_t* __restrict__ pages, const _Float16* kc, const _Float16* vc,
+    const float* __restrict__ q, float* __restrict__ out,
     float* __restrict__ part_o, float2* __restrict__ part_ml, uint32_t* __restrict__ counters,
+    const float* __restrict__ knew, const float* __restrict__ vnew,
+    const uint32_t* __restrict__ kv_slot, _Float16* kw, _Float16* vw,  // kw/vw alias kc/vc
     uint32_t part_o_bytes, uint32_t part_ml_bytes, uint32_t hq, uint32_t hkv,
     uint32_t bpp_shift, uint32_t window, float scale_log2) {
-  __shared__ DecodeShared<NT> sh;
+  static_assert(sizeof(float4) * kWaves * NT * 8 * (kD / 4) >= sizeof(float2) * kMaxChunks * NT * 8,
+                "the final merge stages every chunk's (m, l) in the o buffer");
+  __shared__ DecodeShared<NT, kWaves> sh;
   const AttnItem it = items[blockIdx.x];
   const uint32_t kh = blockIdx.y;
   const int wave = threadIdx.x >> 6;
@@ -125,6 +141,66 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
   const bool lo_half = c >= 8;
   const uint32_t G = hq / hkv;
   const uint32_t nlog = it.nrows * G;  // logical rows in the group
+
+  // Fused append (knew != nullptr): the group's own new rows are stored by the work
+  // item of its last chunk, which holds every block they fall in (the host makes
+  // sure of that), before its waves read them. Only the keys of this kv head.
+  if (knew != nullptr && it.chunk == it.nch - 1) {
+    const uint32_t page_size = 16u << bpp_shift;
+    for (uint32_t i = threadIdx.x; i < it.nrows * 32; i += 64 * kWaves) {
+      const uint32_t row = it.r0 + i / 32, ch = (i / 2) % 16;
+      const bool is_k = (i & 1) == 0;
+      const float* src = (is_k ? knew : vnew) + (static_cast<size_t>(row) * hkv + kh) * kD + ch * 8;
+      const uint32_t slot = kv_slot[row];
+      const uint32_t off = slot & (page_size - 1);
+      const size_t region = (static_cast<size_t>(slot >> (bpp_shift + 4)) * hkv + kh) * page_size * kD;
+      _Float16* dst = is_k ? kw + region + k_offset(off, ch) : vw + region + off * kD + ch * 8;
+      const float4 a = *reinterpret_cast<const float4*>(src);
+      const float4 b = *reinterpret_cast<const float4*>(src + 4);
+      *reinterpret_cast<half8*>(dst) =
+          half8{static_cast<_Float16>(a.x), static_cast<_Float16>(a.y), static_cast<_Float16>(a.z),
+                static_cast<_Float16>(a.w), static_cast<_Float16>(b.x), static_cast<_Float16>(b.y),
+                static_cast<_Float16>(b.z), static_cast<_Float16>(b.w)};
+    }
+    // Stores complete, then the workgroup barrier orders them before every wave's loads
+    // (the waves of a workgroup share one CU and its L1).
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // This wave's share of the item's blocks, [wb0, wb1), in whole quads of blocks
+  // (at most 64 blocks: one page id per lane).
+  const uint32_t nall = it.blk1 - it.blk0;
+  const uint32_t quads = (nall + 3) / 4;
+  const uint32_t wb0 = it.blk0 + 4 * (quads * wave / kWaves);
+  const uint32_t wb1 = min(it.blk1, it.blk0 + 4 * (quads * (wave + 1) / kWaves));
+  const uint32_t nblk = wb1 > wb0 ? wb1 - wb0 : 0;
+  // Page ids of those blocks, one per lane; block b reads its page back with readlane.
+  const uint32_t bpp_mask = (1u << bpp_shift) - 1u;  // blocks per page - 1
+  const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;  // halves per (page, head)
+  const uint32_t* pt = pages + it.pt_off;
+  int pid = 0;
+  if (static_cast<uint32_t>(lane) < nblk) pid = static_cast<int>(pt[(wb0 + lane) >> bpp_shift]);
+  auto block_off = [&](uint32_t b) -> size_t {  // b relative to wb0, clamped
+    b = b < nblk ? b : nblk - 1;
+    const uint32_t page = static_cast<uint32_t>(__builtin_amdgcn_readlane(pid, static_cast<int>(b)));
+    return (static_cast<size_t>(page) * hkv + kh) * head_stride +
+           static_cast<size_t>((wb0 + b) & bpp_mask) * 16 * kD;
+  };
+  const int key_end = static_cast<int>(wb1 * 16);
+
+  // Two register sets of two blocks each, used in turn: the loads of one set are in
+  // flight while the other is computed.
+  BlockRegs s0[2], s1[2];
+  auto load_pair = [&](BlockRegs* r, uint32_t b) {
+    const size_t o0 = block_off(b), o1 = block_off(b + 1);
+    load_block(r[0], kc + o0, vc + o0, lane);
+    load_block(r[1], kc + o1, vc + o1, lane);
+    // Keep the loads here: the scheduler would otherwise sink them below the compute
+    // of the other set, leaving nothing in flight while it runs.
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if (nblk > 0) load_pair(s0, 0);  // first, so HBM is busy while q is set up
 
   // Per tile: this lane's column's row position and key window, and the q operand.
   half8 qb[NT][4];
@@ -167,36 +243,6 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
     for (int j = 0; j < 8; ++j) acc[t][j] = floatx4{0, 0, 0, 0};
   }
 
-  // This wave's share of the work item's blocks: [wb0, wb1), at most 64 of them.
-  const uint32_t nall = it.blk1 - it.blk0;
-  const uint32_t wb0 = it.blk0 + nall * wave / kWaves;
-  const uint32_t wb1 = it.blk0 + nall * (wave + 1) / kWaves;
-  const uint32_t nblk = wb1 - wb0;
-  // Page ids of those blocks, one per lane; block b reads its page back with readlane.
-  const uint32_t bpp_mask = (1u << bpp_shift) - 1u;  // blocks per page - 1
-  const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;  // halves per (page, head)
-  const uint32_t* pt = pages + it.pt_off;
-  int pid = 0;
-  if (static_cast<uint32_t>(lane) < nblk) pid = static_cast<int>(pt[(wb0 + lane) >> bpp_shift]);
-  auto block_off = [&](uint32_t b) -> size_t {  // b relative to wb0, clamped
-    b = b < nblk ? b : nblk - 1;
-    const uint32_t page = static_cast<uint32_t>(__builtin_amdgcn_readlane(pid, static_cast<int>(b)));
-    return (static_cast<size_t>(page) * hkv + kh) * head_stride +
-           static_cast<size_t>((wb0 + b) & bpp_mask) * 16 * kD;
-  };
-  const int key_end = static_cast<int>(wb1 * 16);
-
-  // Two register sets of two blocks each, used in turn: the loads of one set are in
-  // flight while the other is computed.
-  BlockRegs s0[2], s1[2];
-  auto load_pair = [&](BlockRegs* r, uint32_t b) {
-    const size_t o0 = block_off(b), o1 = block_off(b + 1);
-    load_block(r[0], kc + o0, vc + o0, lane);
-    load_block(r[1], kc + o1, vc + o1, lane);
-    // Keep the loads here: the scheduler would otherwise sink them below the compute
-    // of the other set, leaving nothing in flight while it runs.
-    __builtin_amdgcn_sched_barrier(0);
-  };
   auto process_pair = [&](const BlockRegs* r, uint32_t b) {
     const int kb0 = static_cast<int>((wb0 + b) * 16) + 4 * g;
 #pragma unroll
@@ -253,15 +299,23 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
   };
 
   if (nblk > 0) {
-    // Loads are issued unconditionally (past the end they re-read the last block) so
-    // that every path through the loop has the same loads outstanding and the waits
-    // before each use stay partial.
-    load_pair(s0, 0);
-    for (uint32_t b = 0; b < nblk; b += 4) {
+    // In the loop, loads and compute are unconditional: a conditional use would let the
+    // compiler sink the prefetch into it, and every path keeps the same loads in flight
+    // so the waits before each use stay partial. The last quad is peeled so that no
+    // load is issued past the end.
+    uint32_t b = 0;
+    for (; b + 4 < nblk; b += 4) {
       load_pair(s1, b + 2);
       process_pair(s0, b);
       load_pair(s0, b + 4);
-      if (b + 2 < nblk) process_pair(s1, b + 2);
+      process_pair(s1, b + 2);
+    }
+    if (b + 2 < nblk) {
+      load_pair(s1, b + 2);
+      process_pair(s0, b);
+      process_pair(s1, b + 2);
+    } else {
+      process_pair(s0, b);
     }
   }
 
@@ -294,11 +348,12 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
   const size_t slot = (static_cast<size_t>(it.part_base) + it.chunk) * hkv + kh;
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(part_o, part_o_bytes);
   const __amdgpu_buffer_rsrc_t rml = make_rsrc(part_ml, part_ml_bytes);
+  constexpr int kPer = (NT * 256 + 64 * kWaves - 1) / (64 * kWaves);
 #pragma unroll
-  for (int k = 0; k < NT; ++k) {
+  for (int k = 0; k < kPer; ++k) {
     const uint32_t idx = threadIdx.x + k * 64 * kWaves;
     const uint32_t lr = idx >> 5, qi = idx & 31;
-    if (lr >= nlog) continue;
+    if (lr >= nlog || lr >= NT * 8) continue;
     float mt = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) mt = fmaxf(mt, sh.m[w][lr]);
@@ -328,8 +383,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
   }
   if (it.nch == 1) return;
 
-  // The last work item of this (group, kv head) to arrive merges all of them, in chunk
-  // order (so the result does not depend on the arrival order).
+  // The last work item of this (group, kv head) to arrive merges all of them.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   uint32_t* cnt = counters + static_cast<size_t>(it.counter) * hkv + kh;
@@ -341,23 +395,29 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
   __syncthreads();
   if (!sh.last) return;
 
+  // Every chunk's (m, l) into LDS in one parallel pass, then each thread merges one
+  // (row, 4 dims) over the chunks in chunk order.
   const size_t base0 = static_cast<size_t>(it.part_base) * hkv + kh;
+  float2* ml_all = reinterpret_cast<float2*>(&sh.o[0][0][0]);  // [chunk][row]
+  for (uint32_t i = threadIdx.x; i < it.nch * nlog; i += 64 * kWaves) {
+    const uint32_t ch = i / nlog, lr = i % nlog;
+    const size_t e = (base0 + static_cast<size_t>(ch) * hkv) * rows_per_slot + lr;
+    ml_all[i] = ld2_coherent(rml, static_cast<uint32_t>(e * 8));
+  }
+  __syncthreads();
 #pragma unroll
-  for (int k = 0; k < NT; ++k) {
+  for (int k = 0; k < kPer; ++k) {
     const uint32_t idx = threadIdx.x + k * 64 * kWaves;
     const uint32_t lr = idx >> 5, qi = idx & 31;
-    if (lr >= nlog) continue;
+    if (lr >= nlog || lr >= NT * 8) continue;
     float mt = -INFINITY;
-    for (uint32_t ch = 0; ch < it.nch; ++ch) {
-      const size_t e = (base0 + static_cast<size_t>(ch) * hkv) * rows_per_slot + lr;
-      mt = fmaxf(mt, ld2_coherent(rml, static_cast<uint32_t>(e * 8)).x);
-    }
+    for (uint32_t ch = 0; ch < it.nch; ++ch) mt = fmaxf(mt, ml_all[ch * nlog + lr].x);
     float lt = 0.0f;
     float4 o = {0, 0, 0, 0};
-#pragma unroll 4
+#pragma unroll 8
     for (uint32_t ch = 0; ch < it.nch; ++ch) {
+      const float2 ml = ml_all[ch * nlog + lr];
       const size_t e = (base0 + static_cast<size_t>(ch) * hkv) * rows_per_slot + lr;
-      const float2 ml = ld2_coherent(rml, static_cast<uint32_t>(e * 8));
       const float4 po = ld4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4));
       const float wt = ml.y > 0.0f ? __builtin_amdgcn_exp2f(ml.x - mt) : 0.0f;
       lt += ml.y * wt;

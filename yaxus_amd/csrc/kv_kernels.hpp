@@ -1,16 +1,28 @@
 // K/V store, page copy and data-fill kernels for the paged arena.
 //
-// Arena layout per layer: K and V each `[page][kv_head][page_size][128]` binary16.
+// Arena layout per layer, binary16: V is `[page][kv_head][page_size][128]`; K is the
+// same but each 16-key block of a (page, kv head) is stored `[4][16 keys][32 dims]`:
+// dim d of key k of the block sits at (d / 32) * 512 + k * 32 + d % 32. That is the
+// order in which the attention kernel's MFMA operand loads read it (1 KiB contiguous
+// per load instruction).
+
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace yx {
 
+// Offset in halves of (key `off` of a page, dim chunk `ch` of 8 dims) within a
+// (page, kv head) region of K.
+__host__ __device__ inline size_t k_offset(uint32_t off, uint32_t ch) {
+  return static_cast<size_t>(off / 16) * 2048 + (ch / 4) * 512 + (off % 16) * 32 + (ch % 4) * 8;
+}
+
 // The K/V store of write_rows (crates/yaxus-backend-cpu/src/lib.rs:378-383): one
 // thread per 8 consecutive dims of one (row, kv head); two 16-byte f32 loads, a
 // round-to-nearest-even conversion, one 16-byte store. blockIdx.y: 0 = K, 1 = V.
-// 16 consecutive threads write one 256-byte key row.
+// 16 consecutive threads write one key's 256 bytes (V: one contiguous row; K: four
+// contiguous 64-byte pieces).
 __global__ __launch_bounds__(256) void kv_append_f16(const float* __restrict__ k,
                                                      const float* __restrict__ v,
                                                      const uint32_t* __restrict__ kv_slot,
@@ -22,10 +34,10 @@ __global__ __launch_bounds__(256) void kv_append_f16(const float* __restrict__ k
   if (tid >= rows * per_row) return;
   const uint32_t row = tid / per_row, rem = tid % per_row, h = rem / 16, ch = rem % 16;
   const float* src = (blockIdx.y == 0 ? k : v) + (static_cast<size_t>(row) * hkv + h) * 128 + ch * 8;
-  _Float16* base = blockIdx.y == 0 ? kc : vc;
   const uint32_t slot = kv_slot[row];
   const uint32_t page = slot / page_size, off = slot % page_size;
-  _Float16* dst = base + ((static_cast<size_t>(page) * hkv + h) * page_size + off) * 128 + ch * 8;
+  const size_t region = (static_cast<size_t>(page) * hkv + h) * page_size * 128;
+  _Float16* dst = blockIdx.y == 0 ? kc + region + k_offset(off, ch) : vc + region + off * 128 + ch * 8;
   const float4 a = *reinterpret_cast<const float4*>(src);
   const float4 b = *reinterpret_cast<const float4*>(src + 4);
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));

@@ -109,6 +109,7 @@ struct AttnPlan {
   int nt = 1;
   std::vector<yx::AttnItem> items;
   DevBuf d_items;
+  bool fusable = false;  // the append can run inside the attention kernel
   size_t slots = 0;     // partial slots (per kv head)
   size_t counters = 0;  // arrival counters (per kv head)
 };
@@ -161,7 +162,7 @@ struct yx_ctx {
   DevBuf part_o, part_ml, counters, io_a, io_b, io_c;
   // options
   long target_waves = 2048;
-  long max_chunk_blocks = 64 * yx::kWaves;
+  long max_chunk_blocks = 1 << 20;
   bool profiling = false;
   Profile prof[3];
 
@@ -242,25 +243,30 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
     }
   }
   work *= hkv;
-  // Work items (workgroups of kWaves waves) aimed at: target_waves / kWaves.
-  const size_t target_items = std::max<size_t>(1, static_cast<size_t>(c->target_waves) / yx::kWaves);
+  // Work items (workgroups of DecodeWaves waves) aimed at: target_waves / waves.
+  const size_t waves = nt <= 2 ? yx::DecodeWaves<1>::value : yx::DecodeWaves<4>::value;
+  const size_t target_items = std::max<size_t>(1, static_cast<size_t>(c->target_waves) / waves);
   size_t cb = (work + target_items - 1) / target_items;
-  cb = std::max<size_t>(1, std::min<size_t>(cb, static_cast<size_t>(c->max_chunk_blocks)));
+  // Each wave's page ids fit its 64 lanes.
+  cb = std::max<size_t>(1, std::min<size_t>({cb, static_cast<size_t>(c->max_chunk_blocks), 64 * waves}));
 
   AttnPlan plan;
   plan.nt = static_cast<int>(nt);
   size_t slot = 0;
   for (size_t si = 0; si < subs.size(); ++si) {
     const Sub& s = subs[si];
-    const uint32_t nblk = s.b1 - s.b0;
-    const uint32_t nch = static_cast<uint32_t>((nblk + cb - 1) / cb);
+    // Chunks start on quads of blocks (the waves split them in quads), at most
+    // kMaxChunks of them.
+    const uint32_t nq = (s.b1 - s.b0 + 3) / 4;
+    const uint32_t cq = static_cast<uint32_t>(std::max<size_t>((cb + 3) / 4, (nq + yx::kMaxChunks - 1) / yx::kMaxChunks));
+    const uint32_t nch = (nq + cq - 1) / cq;
     for (uint32_t ch = 0; ch < nch; ++ch) {
       yx::AttnItem w{};
       w.r0 = s.r0;
       w.nrows = s.n;
       w.pt_off = s.pt_off;
-      w.blk0 = s.b0 + static_cast<uint32_t>(static_cast<uint64_t>(nblk) * ch / nch);
-      w.blk1 = s.b0 + static_cast<uint32_t>(static_cast<uint64_t>(nblk) * (ch + 1) / nch);
+      w.blk0 = s.b0 + 4 * static_cast<uint32_t>(static_cast<uint64_t>(nq) * ch / nch);
+      w.blk1 = std::min(s.b1, s.b0 + 4 * static_cast<uint32_t>(static_cast<uint64_t>(nq) * (ch + 1) / nch));
       w.chunk = ch;
       w.nch = nch;
       w.part_base = static_cast<uint32_t>(slot);
@@ -268,6 +274,22 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
       plan.items.push_back(w);
     }
     if (nch > 1) slot += nch;
+  }
+  // The fused append needs each group in one sub and the last chunk of each group to
+  // hold all of its rows' keys (the first row's position is the smallest).
+  plan.fusable = true;
+  {
+    size_t gi = 0;
+    for (const Sub& sb : subs) {
+      while (c->groups[gi].r0 + c->groups[gi].n <= sb.r0) ++gi;
+      if (sb.n != c->groups[gi].n) plan.fusable = false;
+    }
+    for (const yx::AttnItem& w : plan.items) {
+      if (w.chunk + 1 != w.nch) continue;
+      uint32_t pmin = UINT32_MAX;
+      for (uint32_t i = w.r0; i < w.r0 + w.nrows; ++i) pmin = std::min(pmin, c->pos[i]);
+      if (w.blk0 * 16 > pmin) plan.fusable = false;
+    }
   }
   plan.slots = slot;
   plan.counters = subs.size();
@@ -283,8 +305,13 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   return YX_OK;
 }
 
+int append_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v);
+
+// Attention of the pass's rows; with knew/vnew, the rows' K/V are stored first (in
+// the same kernel when the plan allows it, else by the append kernel before it).
 int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* out, size_t hq,
-                   size_t hkv, size_t window, float scale) {
+                   size_t hkv, size_t window, float scale, const float* knew = nullptr,
+                   const float* vnew = nullptr) {
   int rc = check_kv(c, kv, layer);
   if (rc) return rc;
   if (hkv != kv->hkv) return fail(YX_ERR_INVALID, "hkv differs from the arena's");
@@ -299,6 +326,10 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     return rc;
   if ((rc = c->counters.ensure(std::max<size_t>(1, plan->counters * hkv * 4), c->stream, true)))
     return rc;
+  if (knew && !plan->fusable) {
+    if ((rc = append_impl(c, kv, layer, knew, vnew))) return rc;
+    knew = vnew = nullptr;
+  }
   const float scale_log2 = scale * yx::kLog2e;
   dim3 grid(static_cast<unsigned>(plan->items.size()), static_cast<unsigned>(hkv));
   hipEvent_t e0;
@@ -315,11 +346,12 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   const uint32_t W = static_cast<uint32_t>(window);
   const uint32_t po_bytes = static_cast<uint32_t>(std::min<size_t>(c->part_o.cap, 0xffffffffu));
   const uint32_t pml_bytes = static_cast<uint32_t>(std::min<size_t>(c->part_ml.cap, 0xffffffffu));
-  const dim3 block(64 * yx::kWaves);
 #define YX_LAUNCH_DECODE(NT)                                                                        \
-  hipLaunchKernelGGL(yx::paged_attn_decode<NT>, grid, block, 0, c->stream, items, pos, pages,      \
-                     kv->k[layer], kv->v[layer], q, out, po, pml, cnt, po_bytes, pml_bytes, H, HK, \
-                     P, W, scale_log2)
+  hipLaunchKernelGGL(yx::paged_attn_decode<NT>, grid, dim3(64 * yx::DecodeWaves<NT>::value), 0,      \
+                     c->stream, items, pos, pages,                                                  \
+                     kv->k[layer], kv->v[layer], q, out, po, pml, cnt, knew, vnew,                 \
+                     static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],       \
+                     po_bytes, pml_bytes, H, HK, P, W, scale_log2)
   switch (plan->nt) {
     case 1: YX_LAUNCH_DECODE(1); break;
     case 2: YX_LAUNCH_DECODE(2); break;
@@ -415,7 +447,7 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
   if (!std::strcmp(key, "attn_target_waves"))
     c->target_waves = value;
   else if (!std::strcmp(key, "attn_max_chunk_blocks"))
-    c->max_chunk_blocks = std::min<long>(value, 64 * yx::kWaves);  // each wave's page ids fit its 64 lanes
+    c->max_chunk_blocks = value;
   else
     return fail(YX_ERR_INVALID, std::string("unknown option ") + key);
   for (auto& kv : c->plans) kv.second.d_items.release();
@@ -529,21 +561,50 @@ int yx_kv_copy_pages(yx_ctx* c, yx_kv* kv, const uint32_t* src, const uint32_t* 
   return YX_OK;
 }
 
+// Page contents through the host in the logical layout [hkv][page_size][128]; K is
+// converted from / to the arena's block order (k_offset).
 static int page_io(yx_ctx* c, yx_kv* kv, size_t layer, const uint32_t* pages, size_t n, void* k,
                    void* v, bool read) {
   if (!c || !kv || layer >= kv->layers) return fail(YX_ERR_INVALID, "bad arena or layer");
   int rc = c->set_device();
   if (rc) return rc;
   const size_t pb = kv->page_bytes();
+  const size_t ph = pb / 2;  // halves per page
+  std::vector<uint16_t> tmp(ph);
+  auto permute = [&](const uint16_t* logical, uint16_t* arena, bool to_arena) {
+    for (size_t h = 0; h < kv->hkv; ++h)
+      for (uint32_t off = 0; off < kv->page; ++off)
+        for (uint32_t ch = 0; ch < 16; ++ch) {
+          const size_t region = h * kv->page * 128;
+          const uint16_t* src;
+          uint16_t* dst;
+          if (to_arena) {
+            src = logical + region + off * 128 + ch * 8;
+            dst = arena + region + yx::k_offset(off, ch);
+          } else {
+            src = arena + region + yx::k_offset(off, ch);
+            dst = const_cast<uint16_t*>(logical) + region + off * 128 + ch * 8;
+          }
+          std::memcpy(dst, src, 16);
+        }
+  };
   for (size_t i = 0; i < n; ++i) {
     if (pages[i] >= kv->pages) return fail(YX_ERR_INVALID, "page beyond the arena");
     char* kd = reinterpret_cast<char*>(kv->k[layer]) + pages[i] * pb;
     char* vd = reinterpret_cast<char*>(kv->v[layer]) + pages[i] * pb;
     if (read) {
-      if (k) YX_HIP(hipMemcpyAsync(static_cast<char*>(k) + i * pb, kd, pb, hipMemcpyDeviceToHost, c->stream));
+      if (k) {
+        YX_HIP(hipMemcpyAsync(tmp.data(), kd, pb, hipMemcpyDeviceToHost, c->stream));
+        YX_HIP(hipStreamSynchronize(c->stream));
+        permute(reinterpret_cast<uint16_t*>(static_cast<char*>(k) + i * pb), tmp.data(), false);
+      }
       if (v) YX_HIP(hipMemcpyAsync(static_cast<char*>(v) + i * pb, vd, pb, hipMemcpyDeviceToHost, c->stream));
     } else {
-      if (k) YX_HIP(hipMemcpyAsync(kd, static_cast<const char*>(k) + i * pb, pb, hipMemcpyHostToDevice, c->stream));
+      if (k) {
+        permute(reinterpret_cast<const uint16_t*>(static_cast<const char*>(k) + i * pb), tmp.data(), true);
+        YX_HIP(hipMemcpyAsync(kd, tmp.data(), pb, hipMemcpyHostToDevice, c->stream));
+        YX_HIP(hipStreamSynchronize(c->stream));
+      }
       if (v) YX_HIP(hipMemcpyAsync(vd, static_cast<const char*>(v) + i * pb, pb, hipMemcpyHostToDevice, c->stream));
     }
   }
@@ -663,6 +724,42 @@ int yx_attention(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* out,
                              static_cast<float*>(c->io_c.p), hq, hkv, window, scale)))
     return rc;
   YX_HIP(hipMemcpyAsync(out, c->io_c.p, bytes, hipMemcpyDeviceToHost, c->stream));
+  YX_HIP(hipStreamSynchronize(c->stream));
+  return YX_OK;
+}
+
+int yx_attention_append_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v,
+                            const float* q, float* out, size_t hq, size_t hkv, size_t window,
+                            float scale) {
+  if (!c || !kv) return fail(YX_ERR_INVALID, "null argument");
+  if (!k || !v) return fail(YX_ERR_INVALID, "null k or v");
+  int rc = c->set_device();
+  if (rc) return rc;
+  for (size_t i = 0; i < c->rows; ++i)
+    if ((c->pos[i] / kv->page) + c->pt_off[i] >= c->npages)
+      return fail(YX_ERR_INVALID, "a row's position has no page-table entry");
+  return attention_impl(c, kv, layer, q, out, hq, hkv, window, scale, k, v);
+}
+
+int yx_attention_append(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v,
+                        const float* q, float* out, size_t hq, size_t hkv, size_t window,
+                        float scale) {
+  if (!c || !kv) return fail(YX_ERR_INVALID, "null argument");
+  int rc = c->set_device();
+  if (rc) return rc;
+  const size_t qb = c->rows * hq * 128 * 4, kb = c->rows * kv->hkv * 128 * 4;
+  if ((rc = c->io_a.ensure(std::max<size_t>(qb, 16), c->stream))) return rc;
+  if ((rc = c->io_b.ensure(std::max<size_t>(2 * kb, 16), c->stream))) return rc;
+  if ((rc = c->io_c.ensure(std::max<size_t>(qb, 16), c->stream))) return rc;
+  float* dk = static_cast<float*>(c->io_b.p);
+  float* dv = dk + c->rows * kv->hkv * 128;
+  YX_HIP(hipMemcpyAsync(c->io_a.p, q, qb, hipMemcpyHostToDevice, c->stream));
+  YX_HIP(hipMemcpyAsync(dk, k, kb, hipMemcpyHostToDevice, c->stream));
+  YX_HIP(hipMemcpyAsync(dv, v, kb, hipMemcpyHostToDevice, c->stream));
+  if ((rc = yx_attention_append_dev(c, kv, layer, dk, dv, static_cast<float*>(c->io_a.p),
+                                    static_cast<float*>(c->io_c.p), hq, hkv, window, scale)))
+    return rc;
+  YX_HIP(hipMemcpyAsync(out, c->io_c.p, qb, hipMemcpyDeviceToHost, c->stream));
   YX_HIP(hipStreamSynchronize(c->stream));
   return YX_OK;
 }
