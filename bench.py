@@ -34,7 +34,7 @@ O_BYTES = B * HQ * D * 4
 PT_BYTES = B * (CTX // PAGE) * 4
 APPEND_BYTES = B * HKV * D * 2 * 2
 LAYER_STEP_BYTES = KV_BYTES + Q_BYTES + O_BYTES + PT_BYTES + APPEND_BYTES
-ATTN_BYTES = KV_BYTES + Q_BYTES + O_BYTES + PT_BYTES
+ATTN_BYTES = LAYER_STEP_BYTES  # the fused kernel stores the appended K/V too
 METRIC = "paged decode-attn GB/s (% HBM peak) + µs/layer-step at B=16, ctx 4096"
 SEED = 0x59415855
 
@@ -111,6 +111,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile-run", action="store_true",
+                    help="for rocprofv3: also run a 1 GiB device copy (the byte-counter "
+                         "calibration point) and skip the CPU baseline")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch the 24 layers one call at a time instead of replaying a HIP graph")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -151,9 +156,19 @@ def main():
     for _ in range(args.warmup):
         step()
     hip.sync()
+    if not args.no_graph:
+        # One decode step (24 layers) as a HIP graph, replayed per step.
+        hip.graph_begin()
+        step()
+        hip.graph_end()
+        hip.graph_launch()
+        hip.sync()
     hip.timer_start()
     for _ in range(args.steps):
-        step()
+        if args.no_graph:
+            step()
+        else:
+            hip.graph_launch()
     ms = hip.timer_stop()
     ms_per_step = ms / args.steps
     us_layer = ms_per_step * 1000.0 / LAYERS
@@ -168,6 +183,14 @@ def main():
     for _ in range(args.steps):
         step()
     hip.profile(False)
+    if args.profile_run:
+        # Calibration for FETCH_SIZE / WRITE_SIZE: a plain copy of exactly 1 GiB.
+        src, dst = hip.tensor((1 << 30,), np.uint8), hip.tensor((1 << 30,), np.uint8)
+        for _ in range(3):
+            hip.L.yx_dev_copy(hip.ctx, dst.ptr, src.ptr, 1 << 30)
+        hip.sync()
+        src.free()
+        dst.free()
     attn_ms, attn_n = hip.profile_read(YX_KERNEL_ATTENTION)
     attn_us = attn_ms / max(attn_n, 1) * 1000.0
     achieved = ATTN_BYTES / (attn_us * 1e-6) / 1e9
@@ -186,6 +209,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
+        "launch": "per-call" if args.no_graph else "hip-graph (one graph per 24-layer step)",
         "data": "synthetic (splitmix64/Box-Muller N(0,1), seed 0x59415855)",
         "config": {
             "workload": "batched paged decode: B=16, ctx 4096, 16q/4kv heads, d 128, "
@@ -195,7 +219,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_attn_decode<1>",
+            "kernel": "paged_attn_decode<1,8> (fused append + attention)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -204,7 +228,7 @@ def main():
             "bytes_per_launch": ATTN_BYTES,
             "traffic": traffic_from_profiles(),
         },
-        "cpu_baseline": None if args.no_cpu else cpu_baseline(pr, args.cpu_seconds),
+        "cpu_baseline": None if (args.no_cpu or args.profile_run) else cpu_baseline(pr, args.cpu_seconds),
     }
     print(json.dumps(line), flush=True)
     hip.close()

@@ -112,6 +112,13 @@ int yx_dev_copy(yx_ctx* ctx, void* dst, const void* src, size_t bytes);
  * index offset + i (see yaxus_amd/data.py for the definition); dtype f32 or f16. */
 int yx_fill_normal(yx_ctx* ctx, void* dst, size_t n, int dtype, uint64_t seed, uint64_t offset);
 
+/* HIP graph of the calls made between begin and end on the context's stream (each
+ * must have run once before, so its work list is on the device); launch replays it.
+ * The kernels leave their arrival counters at zero, so replays need no memset. */
+int yx_graph_begin(yx_ctx* ctx);
+int yx_graph_end(yx_ctx* ctx);
+int yx_graph_launch(yx_ctx* ctx);
+
 /* Timing with HIP events on the context's stream. */
 int yx_timer_start(yx_ctx* ctx);
 int yx_timer_stop(yx_ctx* ctx, float* ms);

@@ -150,3 +150,18 @@ def test_fused_append_attention(hip, hq, hkv, k, window):
     assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
     used = sorted(set(int(p) for s in seqs for p in sc.cache.seq_pages(s)))
     _check_pages(sc, 0, used)
+
+
+def test_attention_is_deterministic(hip):
+    """Chunks are merged in chunk order and each wave's blocks are fixed: two runs of
+    the same pass give the same bits."""
+    hq, hkv = 16, 4
+    sc = Scenario(hip, pages=800, page=16, hkv=hkv, pool_seed=8)
+    seqs = [sc.cache.new_seq() for _ in range(8)]
+    sc.prefill(dict(zip(seqs, [4000, 3000, 2047, 100, 1, 555, 1024, 700])))
+    pr = sc.run_pass([(s, 1) for s in seqs])
+    sc.store(pr)
+    q = sc.draw(8 * hq * D).reshape(8, hq * D)
+    a = hip.attend(sc.kv, 0, q, hq)
+    b = hip.attend(sc.kv, 0, q, hq)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

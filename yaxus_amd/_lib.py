@@ -91,6 +91,9 @@ HIP_SYMBOLS = {
     "yx_memcpy_d2h": (I, [P, P, P, S]),
     "yx_dev_copy": (I, [P, P, P, S]),
     "yx_fill_normal": (I, [P, P, S, I, U64, U64]),
+    "yx_graph_begin": (I, [P]),
+    "yx_graph_end": (I, [P]),
+    "yx_graph_launch": (I, [P]),
     "yx_timer_start": (I, [P]),
     "yx_timer_stop": (I, [P, P]),
     "yx_profile_enable": (I, [P, I]),

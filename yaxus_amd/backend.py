@@ -203,6 +203,15 @@ class HipBackend:
                                         _lib.YX_DTYPE_F16 if f16 else _lib.YX_DTYPE_F32,
                                         seed, offset))
 
+    def graph_begin(self):
+        check_hip(self.L.yx_graph_begin(self.ctx))
+
+    def graph_end(self):
+        check_hip(self.L.yx_graph_end(self.ctx))
+
+    def graph_launch(self):
+        check_hip(self.L.yx_graph_launch(self.ctx))
+
     def timer_start(self):
         check_hip(self.L.yx_timer_start(self.ctx))
 

@@ -54,7 +54,7 @@ struct AttnItem {
 
 static constexpr float kLog2e = 1.4426950408889634f;
 static constexpr int kD = 128;
-static constexpr uint32_t kMaxChunks = 64;
+static constexpr uint32_t kMaxChunks = 256;
 
 // Lane l reads lane l^8 (DPP row rotate by 8 within each row of 16 lanes).
 __device__ __forceinline__ float xor8(float x) {
@@ -116,7 +116,7 @@ template <int NT, int W>
 struct DecodeShared {
   float m[W][NT * 8];
   float l[W][NT * 8];
-  float4 o[W][NT * 8][kD / 4];  // also holds the (m, l) of all chunks in the final merge
+  float4 o[W][NT * 8][kD / 4];
   uint32_t last;
 };
 
@@ -130,8 +130,6 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
     const uint32_t* __restrict__ kv_slot, _Float16* kw, _Float16* vw,  // kw/vw alias kc/vc
     uint32_t part_o_bytes, uint32_t part_ml_bytes, uint32_t hq, uint32_t hkv,
     uint32_t bpp_shift, uint32_t window, float scale_log2) {
-  static_assert(sizeof(float4) * kWaves * NT * 8 * (kD / 4) >= sizeof(float2) * kMaxChunks * NT * 8,
-                "the final merge stages every chunk's (m, l) in the o buffer");
   __shared__ DecodeShared<NT, kWaves> sh;
   const AttnItem it = items[blockIdx.x];
   const uint32_t kh = blockIdx.y;
@@ -168,24 +166,24 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
     __syncthreads();
   }
 
-  // This wave's share of the item's blocks, [wb0, wb1), in whole quads of blocks
-  // (at most 64 blocks: one page id per lane).
+  // This wave's share of the item's blocks, [wb0, wb1), in whole quads of blocks (a
+  // static split: the result does not depend on timing). A chunk has at most 64 blocks:
+  // one page id per lane.
   const uint32_t nall = it.blk1 - it.blk0;
   const uint32_t quads = (nall + 3) / 4;
   const uint32_t wb0 = it.blk0 + 4 * (quads * wave / kWaves);
   const uint32_t wb1 = min(it.blk1, it.blk0 + 4 * (quads * (wave + 1) / kWaves));
   const uint32_t nblk = wb1 > wb0 ? wb1 - wb0 : 0;
-  // Page ids of those blocks, one per lane; block b reads its page back with readlane.
   const uint32_t bpp_mask = (1u << bpp_shift) - 1u;  // blocks per page - 1
   const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;  // halves per (page, head)
   const uint32_t* pt = pages + it.pt_off;
   int pid = 0;
-  if (static_cast<uint32_t>(lane) < nblk) pid = static_cast<int>(pt[(wb0 + lane) >> bpp_shift]);
-  auto block_off = [&](uint32_t b) -> size_t {  // b relative to wb0, clamped
-    b = b < nblk ? b : nblk - 1;
+  if (static_cast<uint32_t>(lane) < nall) pid = static_cast<int>(pt[(it.blk0 + lane) >> bpp_shift]);
+  auto block_off = [&](uint32_t b) -> size_t {  // b relative to wb0, clamped to [wb0, wb1)
+    b = (wb0 - it.blk0) + (b < nblk ? b : nblk - 1);
     const uint32_t page = static_cast<uint32_t>(__builtin_amdgcn_readlane(pid, static_cast<int>(b)));
     return (static_cast<size_t>(page) * hkv + kh) * head_stride +
-           static_cast<size_t>((wb0 + b) & bpp_mask) * 16 * kD;
+           static_cast<size_t>((it.blk0 + b) & bpp_mask) * 16 * kD;
   };
   const int key_end = static_cast<int>(wb1 * 16);
 
@@ -395,36 +393,38 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
   __syncthreads();
   if (!sh.last) return;
 
-  // Every chunk's (m, l) into LDS in one parallel pass, then each thread merges one
-  // (row, 4 dims) over the chunks in chunk order.
+  // Each thread merges one (row, 4 dims) over the chunks in chunk order, with a
+  // running maximum; the loads of 8 chunks are in flight at a time.
   const size_t base0 = static_cast<size_t>(it.part_base) * hkv + kh;
-  float2* ml_all = reinterpret_cast<float2*>(&sh.o[0][0][0]);  // [chunk][row]
-  for (uint32_t i = threadIdx.x; i < it.nch * nlog; i += 64 * kWaves) {
-    const uint32_t ch = i / nlog, lr = i % nlog;
-    const size_t e = (base0 + static_cast<size_t>(ch) * hkv) * rows_per_slot + lr;
-    ml_all[i] = ld2_coherent(rml, static_cast<uint32_t>(e * 8));
-  }
-  __syncthreads();
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const uint32_t idx = threadIdx.x + k * 64 * kWaves;
     const uint32_t lr = idx >> 5, qi = idx & 31;
     if (lr >= nlog || lr >= NT * 8) continue;
-    float mt = -INFINITY;
-    for (uint32_t ch = 0; ch < it.nch; ++ch) mt = fmaxf(mt, ml_all[ch * nlog + lr].x);
-    float lt = 0.0f;
+    float mt = -INFINITY, lt = 0.0f;
     float4 o = {0, 0, 0, 0};
-#pragma unroll 8
-    for (uint32_t ch = 0; ch < it.nch; ++ch) {
-      const float2 ml = ml_all[ch * nlog + lr];
-      const size_t e = (base0 + static_cast<size_t>(ch) * hkv) * rows_per_slot + lr;
-      const float4 po = ld4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4));
-      const float wt = ml.y > 0.0f ? __builtin_amdgcn_exp2f(ml.x - mt) : 0.0f;
-      lt += ml.y * wt;
-      o.x += po.x * wt;
-      o.y += po.y * wt;
-      o.z += po.z * wt;
-      o.w += po.w * wt;
+    for (uint32_t c0 = 0; c0 < it.nch; c0 += 8) {
+      float2 ml[8];
+      float4 po[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t ch = min(c0 + j, it.nch - 1);
+        const size_t e = (base0 + static_cast<size_t>(ch) * hkv) * rows_per_slot + lr;
+        ml[j] = ld2_coherent(rml, static_cast<uint32_t>(e * 8));
+        po[j] = ld4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (c0 + j >= it.nch || !(ml[j].y > 0.0f)) continue;  // past the end, or empty
+        const float mn = fmaxf(mt, ml[j].x);
+        const float r = __builtin_amdgcn_exp2f(mt - mn), wt = __builtin_amdgcn_exp2f(ml[j].x - mn);
+        lt = lt * r + ml[j].y * wt;
+        o.x = o.x * r + po[j].x * wt;
+        o.y = o.y * r + po[j].y * wt;
+        o.z = o.z * r + po[j].z * wt;
+        o.w = o.w * r + po[j].w * wt;
+        mt = mn;
+      }
     }
     const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
     const float inv = 1.0f / lt;

@@ -165,6 +165,9 @@ struct yx_ctx {
   long max_chunk_blocks = 1 << 20;
   bool profiling = false;
   Profile prof[3];
+  bool capturing = false;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
 
   int set_device() {
     YX_HIP(hipSetDevice(device));
@@ -247,8 +250,8 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   const size_t waves = nt <= 2 ? yx::DecodeWaves<1>::value : yx::DecodeWaves<4>::value;
   const size_t target_items = std::max<size_t>(1, static_cast<size_t>(c->target_waves) / waves);
   size_t cb = (work + target_items - 1) / target_items;
-  // Each wave's page ids fit its 64 lanes.
-  cb = std::max<size_t>(1, std::min<size_t>({cb, static_cast<size_t>(c->max_chunk_blocks), 64 * waves}));
+  // A chunk's page ids fit one wave's 64 lanes.
+  cb = std::max<size_t>(1, std::min<size_t>({cb, static_cast<size_t>(c->max_chunk_blocks), 64}));
 
   AttnPlan plan;
   plan.nt = static_cast<int>(nt);
@@ -259,6 +262,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
     // kMaxChunks of them.
     const uint32_t nq = (s.b1 - s.b0 + 3) / 4;
     const uint32_t cq = static_cast<uint32_t>(std::max<size_t>((cb + 3) / 4, (nq + yx::kMaxChunks - 1) / yx::kMaxChunks));
+    if (cq > 16) return fail(YX_ERR_UNSUPPORTED, "context too long: more than 256 chunks of 64 blocks");
     const uint32_t nch = (nq + cq - 1) / cq;
     for (uint32_t ch = 0; ch < nch; ++ch) {
       yx::AttnItem w{};
@@ -318,6 +322,8 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   if (hq == 0 || hq % hkv != 0) return fail(YX_ERR_INVALID, "hq must be a positive multiple of hkv");
   if (c->rows == 0) return YX_OK;
   AttnPlan* plan;
+  if (c->capturing && !c->plans.count(std::make_tuple(window, hq, hkv)))
+    return fail(YX_ERR_INVALID, "run the call once before capturing it (its work list is uploaded then)");
   if ((rc = build_plan(c, window, hq, hkv, &plan))) return rc;
   const size_t rps = static_cast<size_t>(plan->nt) * 8;
   if ((rc = c->part_o.ensure(std::max<size_t>(1, plan->slots * hkv * rps * 128 * 4), c->stream)))
@@ -426,6 +432,8 @@ int yx_ctx_destroy(yx_ctx* c) {
   for (DevBuf* b : {&c->d_pos, &c->d_slot, &c->d_pages, &c->part_o, &c->part_ml, &c->counters,
                     &c->io_a, &c->io_b, &c->io_c})
     b->release();
+  if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+  if (c->graph) (void)hipGraphDestroy(c->graph);
   c->staging[0].release();
   c->staging[1].release();
   (void)hipEventDestroy(c->t0);
@@ -824,6 +832,38 @@ int yx_fill_normal(yx_ctx* c, void* dst, size_t n, int dtype, uint64_t seed, uin
   hipLaunchKernelGGL(yx::fill_normal, dim3(blocks), dim3(256), 0, c->stream, dst, n,
                      dtype == YX_DTYPE_F16 ? 1 : 0, seed, offset);
   YX_HIP(hipGetLastError());
+  return YX_OK;
+}
+
+int yx_graph_begin(yx_ctx* c) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  if (c->capturing) return fail(YX_ERR_INVALID, "already capturing");
+  if (c->profiling) return fail(YX_ERR_INVALID, "profiling events cannot be captured");
+  int rc = c->set_device();
+  if (rc) return rc;
+  YX_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  c->capturing = true;
+  return YX_OK;
+}
+
+int yx_graph_end(yx_ctx* c) {
+  if (!c || !c->capturing) return fail(YX_ERR_INVALID, "not capturing");
+  c->capturing = false;
+  hipGraph_t g = nullptr;
+  YX_HIP(hipStreamEndCapture(c->stream, &g));
+  if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+  if (c->graph) (void)hipGraphDestroy(c->graph);
+  c->graph = g;
+  c->graph_exec = nullptr;
+  YX_HIP(hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0));
+  return YX_OK;
+}
+
+int yx_graph_launch(yx_ctx* c) {
+  if (!c || !c->graph_exec) return fail(YX_ERR_INVALID, "no captured graph");
+  int rc = c->set_device();
+  if (rc) return rc;
+  YX_HIP(hipGraphLaunch(c->graph_exec, c->stream));
   return YX_OK;
 }
 
