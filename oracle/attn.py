@@ -33,6 +33,7 @@ def lib():
         L.orc_copy_page.argtypes = [P, P, ctypes.c_int, S, S, ctypes.c_uint32, ctypes.c_uint32]
         L.orc_attend.argtypes = [P, S, S, S, S, P, P, P, S, S, P, P, ctypes.c_int, P, ctypes.c_int]
         L.orc_attend_f64.argtypes = [P, S, S, S, S, P, P, P, S, S, P, P, ctypes.c_int, P]
+        L.orc_normal.argtypes = [ctypes.c_uint64, ctypes.c_uint64, S, P]
         L.orc_dot.argtypes = [P, P, S]
         L.orc_dot.restype = ctypes.c_float
         _LIB = L
@@ -41,6 +42,14 @@ def lib():
 
 def _p(a):
     return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def normal(n, seed, offset=0):
+    """N(0,1) f32 inputs (splitmix64 -> Box-Muller, glibc libm): the same bits on every
+    host of this image."""
+    out = np.empty(int(n), dtype=np.float32)
+    lib().orc_normal(seed, offset, int(n), _p(out))
+    return out
 
 
 def f32_to_f16_bits(x):

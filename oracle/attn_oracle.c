@@ -346,3 +346,27 @@ void orc_attend_f64(const float* q, size_t rows, size_t hq, size_t hkv, size_t d
       free(sc);
     }
 }
+
+/* ---- seeded inputs ------------------------------------------------------------------ */
+
+static uint64_t orc_splitmix64(uint64_t x) {
+  x += 0x9e3779b97f4a7c15ull;
+  x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+  x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+  return x ^ (x >> 31);
+}
+
+/* N(0,1) values of stream `seed` from element `offset` (the definition in
+ * yaxus_amd/data.py): pair k draws u1, u2 from splitmix64(seed + 2k), (seed + 2k + 1)
+ * (top 53 bits), r = sqrt(-2 ln(1 - u1)), th = 2 pi u2; element 2k = r cos th,
+ * 2k + 1 = r sin th; f64 math (glibc), rounded to f32. */
+void orc_normal(uint64_t seed, uint64_t offset, size_t n, float* out) {
+  for (size_t i = 0; i < n; ++i) {
+    uint64_t e = offset + i, k = e >> 1;
+    double u1 = (double)(orc_splitmix64(seed + 2 * k) >> 11) * 0x1.0p-53;
+    double u2 = (double)(orc_splitmix64(seed + 2 * k + 1) >> 11) * 0x1.0p-53;
+    double r = sqrt(-2.0 * log(1.0 - u1));
+    double th = 6.283185307179586 * u2;
+    out[i] = (float)((e & 1) ? r * sin(th) : r * cos(th));
+  }
+}

@@ -11,7 +11,7 @@ import numpy as np
 
 from oracle.attn import OracleArena
 from yaxus_amd import KvCache
-from yaxus_amd.data import normal
+from oracle.attn import normal
 
 D = 128
 
