@@ -95,6 +95,161 @@ def cpu_baseline(pr, budget_s=10.0):
     }
 
 
+def _fill_arena(hip, kv, layers, seed):
+    from yaxus_amd._lib import YX_K, YX_V
+
+    per = kv.pages * kv.page_bytes // 2
+    for l in range(layers):
+        hip.fill_normal(kv.layer_ptr(l, YX_K), per, True, seed, (2 * l) * per)
+        hip.fill_normal(kv.layer_ptr(l, YX_V), per, True, seed, (2 * l + 1) * per)
+
+
+def _scatter(cache, pool, seed):
+    from yaxus_amd.data import permutation
+
+    holders = [cache.new_seq() for _ in range(pool)]
+    for s in holders:
+        cache.append([(s, [0] * PAGE)], [])
+    for i in permutation(pool, seed):
+        cache.free_seq(holders[int(i)])
+
+
+def _time_layers(hip, kv, pr, layers, hq, windows, steps, extra=None):
+    """Times `steps` passes of `layers` fused append + attention launches on resident
+    inputs (one HIP graph per pass); returns µs per pass."""
+    from yaxus_amd.backend import DeviceTensor  # noqa: F401
+
+    rows = len(pr.meta.pos)
+    q = hip.tensor((rows, hq * D))
+    k = hip.tensor((rows, HKV * D))
+    v = hip.tensor((rows, HKV * D))
+    out = hip.tensor((rows, hq * D))
+    for i, t in enumerate((q, k, v)):
+        hip.fill_normal(t.ptr, t.nbytes // 4, False, SEED + 99, i << 32)
+    hip.begin_pass(pr.meta)
+
+    def one():
+        for l in range(layers):
+            hip.attend_append(kv, l, k, v, q, hq, window=windows[l], out=out)
+
+    one()
+    hip.sync()
+    hip.graph_begin()
+    one()
+    hip.graph_end()
+    hip.graph_launch()
+    hip.sync()
+    hip.timer_start()
+    for _ in range(steps):
+        hip.graph_launch()
+        if extra:
+            extra()
+    us = hip.timer_stop() * 1000.0 / steps
+    for t in (q, k, v, out):
+        t.free()
+    return us
+
+
+def bench_configs(hip, steps=10, include_long=True):
+    """BASELINE configurations 2-5 at full size (one JSON object per configuration)."""
+    from yaxus_amd import KvCache
+    from yaxus_amd.data import uniform_ints
+
+    res = {}
+    # cfg2: 16 requests share a 1024-token prefix (64 refcounted pages); suffixes
+    # U[512, 3072]; one decode step over 24 layers.
+    pool, layers = 4096, 24
+    cache = KvCache(pool, 1 << 20, PAGE)
+    _scatter(cache, pool, SEED + 2)
+    base = cache.new_seq()
+    cache.append([(base, [1] * 1024)], [])
+    suf = uniform_ints(B, 512, 3072, SEED + 2)
+    seqs = [cache.fork(base, 1024, []) for _ in range(B)]
+    for s, n in zip(seqs, suf):
+        cache.append([(s, [1] * int(n))], [])
+    pr = cache.append([(s, [2]) for s in seqs], [])
+    kv = hip.new_kv(layers, pool, PAGE, HKV, D)
+    _fill_arena(hip, kv, layers, SEED + 2)
+    us = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, steps) / layers
+    ctx = [1024 + int(n) + 1 for n in suf]
+    logical = sum(ctx) * HKV * D * 2 * 2
+    unique = (1024 + int(sum(suf)) + B) * HKV * D * 2 * 2
+    res["cfg2_prefix_decode"] = {"us_per_layer_step": round(us, 2),
+                                 "logical_GBs": round(logical / us / 1e3, 1),
+                                 "unique_GBs": round(unique / us / 1e3, 1),
+                                 "logical_bytes": logical, "unique_bytes": unique}
+    kv.destroy()
+    # cfg3: 16 requests append a 256-token chunk on contexts U[0, 2048] that leave a
+    # half-filled tail page; causal within the chunk; 24 layers.
+    pool = 4096
+    cache = KvCache(pool, 1 << 20, PAGE)
+    _scatter(cache, pool, SEED + 3)
+    prior = [int(x) // 16 * 16 + 8 for x in uniform_ints(B, 0, 2040, SEED + 3)]
+    seqs = [cache.new_seq() for _ in range(B)]
+    for s, n in zip(seqs, prior):
+        cache.append([(s, [1] * n)], [])
+    pr = cache.append([(s, [2] * 256) for s in seqs], [])
+    kv = hip.new_kv(layers, pool, PAGE, HKV, D)
+    _fill_arena(hip, kv, layers, SEED + 3)
+    us = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, max(2, steps // 2)) / layers
+    flops = sum(4 * HQ * D * (256 * p + 256 * 257 // 2) for p in prior)
+    res["cfg3_chunked_prefill"] = {"us_per_layer_step": round(us, 2),
+                                   "TFLOPs": round(flops / us / 1e6, 2),
+                                   "mfma_util_vs_2.5PF": round(flops / us / 1e6 / 2500.0, 4),
+                                   "flops_per_layer": flops}
+    kv.destroy()
+    # cfg5: 16 requests of ctx 4096 (2048 shared) verify 5 draft tokens (5 causal
+    # rows each); then 8 fork from a partly filled tail page (copy on write) and roll
+    # back a seeded count in [0, 5]; 24 layers.
+    pool = 8192
+    cache = KvCache(pool, 1 << 20, PAGE)
+    _scatter(cache, pool, SEED + 5)
+    base = cache.new_seq()
+    cache.append([(base, [1] * 2048)], [])
+    seqs = [cache.fork(base, 2048, []) for _ in range(B)]
+    for s in seqs:
+        cache.append([(s, [1] * (4096 - 2048 - 5))], [])
+    pr = cache.append([(s, [2] * 5) for s in seqs], [])
+    kv = hip.new_kv(layers, pool, PAGE, HKV, D)
+    _fill_arena(hip, kv, layers, SEED + 5)
+    us_verify = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, steps) / layers
+    t0 = time.perf_counter()
+    copies = []
+    forks = [cache.fork(s, cache.seq_len(s) - 3, copies) for s in seqs[:8]]
+    back = uniform_ints(len(seqs) + len(forks), 0, 5, SEED + 55)
+    for s, n in zip(seqs + forks, back):
+        cache.truncate(s, cache.seq_len(s) - int(n))
+    host_us = (time.perf_counter() - t0) * 1e6
+    hip.timer_start()
+    hip.copy_pages(kv, copies)
+    copy_us = hip.timer_stop() * 1000.0
+    bytes_verify = sum(4096 for _ in seqs) * HKV * D * 2 * 2
+    res["cfg5_verify_fork"] = {"us_per_layer_step_verify": round(us_verify, 2),
+                               "verify_logical_GBs": round(bytes_verify / us_verify / 1e3, 1),
+                               "fork_copies": len(copies), "copy_us_all_layers": round(copy_us, 2),
+                               "host_fork_rollback_us": round(host_us, 1)}
+    kv.destroy()
+    if include_long:
+        # cfg4: 4 requests of 32768 tokens over a 65536-page pool; 32 layers, 1 full
+        # then 3 sliding (window 2048), repeated.
+        pool, layers = 65536, 32
+        cache = KvCache(pool, 1 << 20, PAGE)
+        _scatter(cache, pool, SEED + 4)
+        seqs = [cache.new_seq() for _ in range(4)]
+        for s in seqs:
+            cache.append([(s, [1] * 32767)], [])
+        pr = cache.append([(s, [2]) for s in seqs], [])
+        kv = hip.new_kv(layers, pool, PAGE, HKV, D)
+        _fill_arena(hip, kv, layers, SEED + 4)
+        windows = [0 if l % 4 == 0 else 2048 for l in range(layers)]
+        us_step = _time_layers(hip, kv, pr, layers, HQ, windows, max(2, steps // 2))
+        nbytes = 4 * (8 * 32768 + 24 * 2048) * HKV * D * 2 * 2
+        res["cfg4_long_sliding"] = {"us_per_step_32_layers": round(us_step, 1),
+                                    "GBs": round(nbytes / us_step / 1e3, 1), "bytes_per_step": nbytes}
+        kv.destroy()
+    return res
+
+
 def traffic_from_profiles():
     """HBM bytes per attention launch from the committed rocprof counter summary."""
     p = os.path.join(ROOT, "profiles", "attn_decode_b16_ctx4096_traffic.json")
@@ -114,6 +269,8 @@ def main():
     ap.add_argument("--profile-run", action="store_true",
                     help="for rocprofv3: also run a 1 GiB device copy (the byte-counter "
                          "calibration point) and skip the CPU baseline")
+    ap.add_argument("--configs", action="store_true",
+                    help="also measure BASELINE configurations 2-5 at full size (adds ~2 min)")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the 24 layers one call at a time instead of replaying a HIP graph")
     args = ap.parse_args()
@@ -230,6 +387,9 @@ def main():
         },
         "cpu_baseline": None if (args.no_cpu or args.profile_run) else cpu_baseline(pr, args.cpu_seconds),
     }
+    if args.configs:
+        kv.destroy()
+        line["configs"] = bench_configs(hip)
     print(json.dumps(line), flush=True)
     hip.close()
 

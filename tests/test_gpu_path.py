@@ -166,3 +166,26 @@ def test_attention_is_deterministic(hip):
     a = hip.attend(sc.kv, 0, q, hq)
     b = hip.attend(sc.kv, 0, q, hq)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("hq,hkv,page,window,chunk", [
+    (16, 4, 16, 0, 256), (16, 4, 16, 100, 64), (8, 8, 16, 0, 40), (32, 2, 128, 0, 96),
+    (16, 4, 128, 300, 33)])
+def test_prefill_tiles_match_oracle(hip, hq, hkv, page, window, chunk):
+    """Chunked prefill (many rows per sequence): the MFMA tile kernel over LDS-staged
+    K/V, causal within the chunk and full (or windowed) over the earlier context."""
+    sc = Scenario(hip, pages=420 if page == 16 else 60, page=page, hkv=hkv, pool_seed=12)
+    prior = [8, 0, 1000, 517]
+    seqs = [sc.cache.new_seq() for _ in prior]
+    sc.prefill({s: n for s, n in zip(seqs, prior) if n})
+    pr = sc.run_pass([(s, chunk) for s in seqs])
+    rows = len(pr.meta.pos)
+    kk = sc.draw(rows * hkv * D).reshape(rows, hkv, D)
+    vv = sc.draw(rows * hkv * D).reshape(rows, hkv, D)
+    q = sc.draw(rows * hq * D).reshape(rows, hq * D)
+    got = hip.attend_append(sc.kv, 0, kk, vv, q, hq, window=window)
+    sc.orc[0].store(pr.meta.kv_slot, kk.reshape(rows, -1), vv.reshape(rows, -1))
+    want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
+    err = np.abs(got - want).max()
+    assert close(got, want).all(), f"max abs err {err}"
+    assert err < 2e-5, f"max abs err {err}"

@@ -256,7 +256,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
         for (int i = 0; i < 4; ++i) {
           const float full = sc[i] + xor8(sc[i]);
           const int kp = kb0 + h * 16 + i;
-          const bool ok = kp >= rlo[t] && kp <= rpos[t] && kp < key_end;
+          const bool ok = (kp >= rlo[t]) & (kp <= rpos[t]) & (kp < key_end);  // no branches
           x[h * 4 + i] = ok ? full * scale_log2 : -INFINITY;
           bmax = fmaxf(bmax, x[h * 4 + i]);
         }

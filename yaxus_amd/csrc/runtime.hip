@@ -13,6 +13,7 @@
 
 #include "../../include/yaxus_hip.h"
 #include "attn_decode.hpp"
+#include "attn_prefill.hpp"
 #include "kv_kernels.hpp"
 
 namespace {
@@ -106,6 +107,8 @@ struct Group {
 
 // A split-K work list for one (window, hq, hkv) over the current pass.
 struct AttnPlan {
+  bool prefill = false;  // MFMA tiles over LDS (many rows per sequence) vs split-K decode
+  std::vector<yx::PrefillItem> pitems;
   int nt = 1;
   std::vector<yx::AttnItem> items;
   DevBuf d_items;
@@ -163,6 +166,7 @@ struct yx_ctx {
   // options
   long target_waves = 2048;
   long max_chunk_blocks = 1 << 20;
+  long prefill_min_rows = 32;
   bool profiling = false;
   Profile prof[3];
   bool capturing = false;
@@ -216,6 +220,45 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   const size_t G = hq / hkv;
   uint32_t max_rows = 0;
   for (const Group& g : c->groups) max_rows = std::max(max_rows, g.n);
+  if (max_rows >= static_cast<uint32_t>(c->prefill_min_rows)) {
+    // Tiles of kPrefillRows logical rows: consecutive rows of one sequence.
+    AttnPlan plan;
+    plan.prefill = true;
+    const uint32_t per = static_cast<uint32_t>(std::max<size_t>(1, yx::kPrefillRows / G));
+    if (G > static_cast<size_t>(yx::kPrefillRows))
+      return fail(YX_ERR_UNSUPPORTED, "more query heads per KV head than a prefill tile holds");
+    for (const Group& g : c->groups)
+      for (uint32_t r = 0; r < g.n; r += per) {
+        yx::PrefillItem w{};
+        w.r0 = g.r0 + r;
+        w.nrows = std::min(per, g.n - r);
+        w.pt_off = g.pt_off;
+        uint32_t lo = UINT32_MAX, hi = 0;
+        for (uint32_t i = w.r0; i < w.r0 + w.nrows; ++i) {
+          const uint32_t p = c->pos[i];
+          lo = std::min(lo, (window > 0 && p + 1 > window) ? p + 1 - static_cast<uint32_t>(window) : 0u);
+          hi = std::max(hi, p);
+        }
+        w.blk0 = lo / 16;
+        w.blk1 = hi / 16 + 1;
+        plan.pitems.push_back(w);
+      }
+    // Longest first: the GPU hands work items to CUs in order as they free up, so
+    // this bounds the busiest CU near the average (contexts differ a lot in a pass).
+    std::stable_sort(plan.pitems.begin(), plan.pitems.end(),
+                     [](const yx::PrefillItem& a, const yx::PrefillItem& b) {
+                       return a.blk1 - a.blk0 > b.blk1 - b.blk0;
+                     });
+    auto& p = c->plans[key];
+    p = std::move(plan);
+    int rc = p.d_items.ensure(p.pitems.size() * sizeof(yx::PrefillItem), c->stream);
+    if (rc) return rc;
+    rc = c->staging[c->cur_staging].upload(p.d_items.p, p.pitems.data(),
+                                           p.pitems.size() * sizeof(yx::PrefillItem), c->stream);
+    if (rc) return rc;
+    *out = &p;
+    return YX_OK;
+  }
   size_t nt = (max_rows * G + 7) / 8;
   nt = std::max<size_t>(1, std::min<size_t>(nt, 4));
   const size_t rows_per_sub = nt * 8 / G;
@@ -332,9 +375,24 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     return rc;
   if ((rc = c->counters.ensure(std::max<size_t>(1, plan->counters * hkv * 4), c->stream, true)))
     return rc;
-  if (knew && !plan->fusable) {
+  if (knew && (plan->prefill || !plan->fusable)) {
     if ((rc = append_impl(c, kv, layer, knew, vnew))) return rc;
     knew = vnew = nullptr;
+  }
+  if (plan->prefill) {
+    uint32_t shift = 0;
+    while ((16u << shift) < kv->page) ++shift;
+    hipEvent_t e0;
+    if ((rc = prof_begin(c, YX_KERNEL_ATTENTION, &e0))) return rc;
+    hipLaunchKernelGGL(yx::paged_attn_prefill, dim3(static_cast<unsigned>(plan->pitems.size()),
+                       static_cast<unsigned>(hkv)), dim3(64 * yx::kPrefillWaves), 0, c->stream,
+                       static_cast<const yx::PrefillItem*>(plan->d_items.p),
+                       static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_pages.p),
+                       kv->k[layer], kv->v[layer], q, out, static_cast<uint32_t>(hq),
+                       static_cast<uint32_t>(hkv), shift, static_cast<uint32_t>(window),
+                       scale * yx::kLog2e);
+    YX_HIP(hipGetLastError());
+    return prof_end(c, YX_KERNEL_ATTENTION, e0);
   }
   const float scale_log2 = scale * yx::kLog2e;
   dim3 grid(static_cast<unsigned>(plan->items.size()), static_cast<unsigned>(hkv));
@@ -454,6 +512,8 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
   if (value < 1) return fail(YX_ERR_INVALID, "option values are positive");
   if (!std::strcmp(key, "attn_target_waves"))
     c->target_waves = value;
+  else if (!std::strcmp(key, "prefill_min_rows"))
+    c->prefill_min_rows = value;
   else if (!std::strcmp(key, "attn_max_chunk_blocks"))
     c->max_chunk_blocks = value;
   else
