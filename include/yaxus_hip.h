@@ -48,8 +48,10 @@ int yx_device_count(int* n);
 int yx_ctx_create(int device, yx_ctx** out);
 int yx_ctx_destroy(yx_ctx* ctx);
 int yx_sync(yx_ctx* ctx);
-/* Tuning knobs: "attn_target_waves" (split-K work items aimed at per launch),
- * "attn_max_chunk_blocks" (most 16-key blocks per work item). */
+/* Tuning knobs: "attn_target_waves" (waves the split-K work list aims at; 0, the
+ * default, means one work item per CU), "attn_max_chunk_blocks" (most 16-key blocks per
+ * work item), "attn_max_tiles" (most 8-row MFMA tiles a decode wave holds, 1-4),
+ * "prefill_min_rows" (rows of one sequence from which the prefill kernel is used). */
 int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
 
 /* Backend::new_kv (lib.rs:118; GPU ops/mod.rs:42-66): `layers` layers of `pages`

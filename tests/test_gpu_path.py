@@ -98,7 +98,7 @@ def test_split_count_does_not_change_results(hip, target_waves):
     try:
         got = hip.attend(sc.kv, 0, q, hq)
     finally:
-        hip.set_option("attn_target_waves", 2048)
+        hip.set_option("attn_target_waves", 0)
     want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
     assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
 

@@ -16,7 +16,7 @@
 // exact and f32 accumulation. Per block of 16 keys:
 //   S^T[key][col] = K[key][:] . Q[col][:]         4 x v_mfma_f32_16x16x32_f16
 //   online softmax per column; P = exp2(S*scale*log2e - m) split into hi/lo f16
-//   O^T[dim][col] += V^T[dim][key] P^T[key][col]  8 x v_mfma_f32_16x16x16_f16
+//   O^T[dim][col] += V^T[dim][key] P^T[key][col]  8 x v_mfma_f32_16x16x32_f16 per 2 blocks
 // Operand layouts (lane l, c = l % 16, g = l / 16):
 //   K: A operand of QK, lane holds key c, dims p*32 + g*8 + 0..7 for MFMA p. The arena
 //      stores each 16-key block of K as [p][key][32 dims] (see kv_kernels.hpp), so the
@@ -105,11 +105,12 @@ __device__ __forceinline__ void load_block(BlockRegs& r, const _Float16* __restr
 }
 
 // Waves per workgroup (W): they share one work item's blocks and merge through LDS.
-// Eight keep twice the loads in flight per CU that four do at this register use; the
-// LDS of the merge limits NT > 2 to four.
+// With one tile a wave needs ~220 registers, so eight waves (two per SIMD) fit a CU and
+// keep twice the loads in flight that four do; more tiles need more than 256 registers
+// per wave, one wave per SIMD, hence four.
 template <int NT>
 struct DecodeWaves {
-  static constexpr int value = NT <= 2 ? 8 : 4;
+  static constexpr int value = NT == 1 ? 8 : 4;
 };
 
 template <int NT, int W>
@@ -265,7 +266,6 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
       bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
       const float mn = fmaxf(m[t], bmax);
       const bool live = mn != -INFINITY;
-      const float corr = live ? __builtin_amdgcn_exp2f(m[t] - mn) : 1.0f;
       float pr[8], rs = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -274,24 +274,28 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
       }
       rs += xor16(rs);
       rs += __shfl_xor(rs, 32);
-      l[t] = l[t] * corr + rs;
+      // Rescale only when some column's maximum moved (wave-uniform test).
+      if (__builtin_amdgcn_ballot_w64(mn != m[t])) {
+        const float corr = live ? __builtin_amdgcn_exp2f(m[t] - mn) : 1.0f;
+        l[t] *= corr;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[t][j] *= corr;
+      }
+      l[t] += rs;
       m[t] = mn;
+      // PV over both blocks at once (16x16x32): element e of the P operand is key
+      // (e / 4) * 16 + 4g + e % 4 of the pair, as in the V operand.
+      half8 pb;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[t][j] *= corr;
+      for (int e = 0; e < 8; ++e) {
+        const _Float16 hi = static_cast<_Float16>(pr[e]);
+        pb[e] = lo_half ? static_cast<_Float16>(pr[e] - static_cast<float>(hi)) : hi;
+      }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        half4 pb;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float pv = pr[h * 4 + i];
-          const _Float16 hi = static_cast<_Float16>(pv);
-          pb[i] = lo_half ? static_cast<_Float16>(pv - static_cast<float>(hi)) : hi;
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const half4 a = {r[h].v[0][j], r[h].v[1][j], r[h].v[2][j], r[h].v[3][j]};
-          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, acc[t][j], 0, 0, 0);
-        }
+      for (int j = 0; j < 8; ++j) {
+        const half8 a = {r[0].v[0][j], r[0].v[1][j], r[0].v[2][j], r[0].v[3][j],
+                         r[1].v[0][j], r[1].v[1][j], r[1].v[2][j], r[1].v[3][j]};
+        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, acc[t][j], 0, 0, 0);
       }
     }
   };

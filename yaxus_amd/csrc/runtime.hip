@@ -164,9 +164,11 @@ struct yx_ctx {
   // scratch
   DevBuf part_o, part_ml, counters, io_a, io_b, io_c;
   // options
-  long target_waves = 2048;
+  long target_waves = 0;  // 0: one work item per CU
+  int cus = 256;
   long max_chunk_blocks = 1 << 20;
   long prefill_min_rows = 32;
+  long max_tiles = 4;
   bool profiling = false;
   Profile prof[3];
   bool capturing = false;
@@ -260,7 +262,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
     return YX_OK;
   }
   size_t nt = (max_rows * G + 7) / 8;
-  nt = std::max<size_t>(1, std::min<size_t>(nt, 4));
+  nt = std::max<size_t>(1, std::min<size_t>(nt, static_cast<size_t>(c->max_tiles)));
   const size_t rows_per_sub = nt * 8 / G;
   if (rows_per_sub == 0) return fail(YX_ERR_UNSUPPORTED, "more than 32 query heads per KV head");
 
@@ -290,8 +292,13 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   }
   work *= hkv;
   // Work items (workgroups of DecodeWaves waves) aimed at: target_waves / waves.
-  const size_t waves = nt <= 2 ? yx::DecodeWaves<1>::value : yx::DecodeWaves<4>::value;
-  const size_t target_items = std::max<size_t>(1, static_cast<size_t>(c->target_waves) / waves);
+  // One workgroup per CU runs at a time for every tile count (8 waves of ~220
+  // registers, or 4 of more than 256), so by default the split aims at one work item
+  // per CU: more would run in a second round.
+  const size_t waves = nt == 1 ? yx::DecodeWaves<1>::value : yx::DecodeWaves<4>::value;
+  const size_t target_items = c->target_waves > 0
+                                  ? std::max<size_t>(1, static_cast<size_t>(c->target_waves) / waves)
+                                  : static_cast<size_t>(c->cus);
   size_t cb = (work + target_items - 1) / target_items;
   // A chunk's page ids fit one wave's 64 lanes.
   cb = std::max<size_t>(1, std::min<size_t>({cb, static_cast<size_t>(c->max_chunk_blocks), 64}));
@@ -465,6 +472,7 @@ int yx_ctx_create(int device, yx_ctx** out) {
     return fail(YX_ERR_UNSUPPORTED, std::string("the kernels are built for gfx950, not ") + prop.gcnArchName);
   auto* c = new yx_ctx();
   c->device = device;
+  c->cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   hipError_t e = hipSetDevice(device);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreate(&c->t0);
@@ -509,9 +517,12 @@ int yx_sync(yx_ctx* c) {
 
 int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
   if (!c || !key) return fail(YX_ERR_INVALID, "null argument");
-  if (value < 1) return fail(YX_ERR_INVALID, "option values are positive");
+  if (value < 0 || (value == 0 && std::strcmp(key, "attn_target_waves")))
+    return fail(YX_ERR_INVALID, "option values are positive (attn_target_waves: 0 = automatic)");
   if (!std::strcmp(key, "attn_target_waves"))
     c->target_waves = value;
+  else if (!std::strcmp(key, "attn_max_tiles"))
+    c->max_tiles = std::min<long>(value, 4);
   else if (!std::strcmp(key, "prefill_min_rows"))
     c->prefill_min_rows = value;
   else if (!std::strcmp(key, "attn_max_chunk_blocks"))
