@@ -168,7 +168,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
   }
 
   // This wave's share of the item's blocks, [wb0, wb1), in whole quads of blocks (a
-  // static split: the result does not depend on timing). A chunk has at most 64 blocks:
+  // static split: the result does not depend on timing); at most 64 blocks per wave,
   // one page id per lane.
   const uint32_t nall = it.blk1 - it.blk0;
   const uint32_t quads = (nall + 3) / 4;
@@ -178,13 +178,13 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
   const uint32_t bpp_mask = (1u << bpp_shift) - 1u;  // blocks per page - 1
   const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;  // halves per (page, head)
   const uint32_t* pt = pages + it.pt_off;
-  int pid = 0;
-  if (static_cast<uint32_t>(lane) < nall) pid = static_cast<int>(pt[(it.blk0 + lane) >> bpp_shift]);
+  int pid = 0;  // page id of block wb0 + lane
+  if (static_cast<uint32_t>(lane) < nblk) pid = static_cast<int>(pt[(wb0 + lane) >> bpp_shift]);
   auto block_off = [&](uint32_t b) -> size_t {  // b relative to wb0, clamped to [wb0, wb1)
-    b = (wb0 - it.blk0) + (b < nblk ? b : nblk - 1);
+    b = b < nblk ? b : nblk - 1;
     const uint32_t page = static_cast<uint32_t>(__builtin_amdgcn_readlane(pid, static_cast<int>(b)));
     return (static_cast<size_t>(page) * hkv + kh) * head_stride +
-           static_cast<size_t>((it.blk0 + b) & bpp_mask) * 16 * kD;
+           static_cast<size_t>((wb0 + b) & bpp_mask) * 16 * kD;
   };
   const int key_end = static_cast<int>(wb1 * 16);
 

@@ -300,8 +300,8 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
                                   ? std::max<size_t>(1, static_cast<size_t>(c->target_waves) / waves)
                                   : static_cast<size_t>(c->cus);
   size_t cb = (work + target_items - 1) / target_items;
-  // A chunk's page ids fit one wave's 64 lanes.
-  cb = std::max<size_t>(1, std::min<size_t>({cb, static_cast<size_t>(c->max_chunk_blocks), 64}));
+  // Each wave's page ids fit its 64 lanes: at most 64 blocks per wave.
+  cb = std::max<size_t>(1, std::min<size_t>({cb, static_cast<size_t>(c->max_chunk_blocks), 64 * waves}));
 
   AttnPlan plan;
   plan.nt = static_cast<int>(nt);
@@ -312,7 +312,8 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
     // kMaxChunks of them.
     const uint32_t nq = (s.b1 - s.b0 + 3) / 4;
     const uint32_t cq = static_cast<uint32_t>(std::max<size_t>((cb + 3) / 4, (nq + yx::kMaxChunks - 1) / yx::kMaxChunks));
-    if (cq > 16) return fail(YX_ERR_UNSUPPORTED, "context too long: more than 256 chunks of 64 blocks");
+    if (cq * 4 > 64 * waves)
+      return fail(YX_ERR_UNSUPPORTED, "context too long for 256 chunks of the widest work item");
     const uint32_t nch = (nq + cq - 1) / cq;
     for (uint32_t ch = 0; ch < nch; ++ch) {
       yx::AttnItem w{};
