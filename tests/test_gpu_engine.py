@@ -1,0 +1,97 @@
+"""The engine driving the HIP path (reference vs_cpu.rs:163-208 `concurrent_matches_solo`,
+restated at the attention level): requests run alone and together give the same
+attention outputs per (request, position), and match the CPU oracle backend."""
+
+import numpy as np
+import pytest
+
+from oracle.attn import OracleArena, normal
+from tests.scenario import close
+from yaxus_amd.engine import Engine, EngineConfig, Request
+from yaxus_amd.model import PagedModel
+
+pytestmark = pytest.mark.gpu
+D, HQ, HKV, LAYERS, PAGE, PAGES = 128, 8, 2, 2, 16, 160
+
+
+def inputs(layer, meta):
+    """k, v, q of each row from (token, position, layer) only."""
+    rows = len(meta.pos)
+    k = np.empty((rows, HKV, D), np.float32)
+    v = np.empty_like(k)
+    q = np.empty((rows, HQ * D), np.float32)
+    for r in range(rows):
+        seed = int(meta.ids[r]) * 1000003 + int(meta.pos[r]) * 31 + layer
+        x = normal((2 * HKV + HQ) * D, seed)
+        k[r] = x[:HKV * D].reshape(HKV, D)
+        v[r] = x[HKV * D:2 * HKV * D].reshape(HKV, D)
+        q[r] = x[2 * HKV * D:]
+    return k, v, q
+
+
+def token_fn(pr, outs):
+    return [(int(p) * 7 + 3) % 97 + 200 for p in pr.meta.pos]
+
+
+class Recording(Engine):
+    def __init__(self, *a, **k):
+        super().__init__(*a, **k)
+        self.m_inputs = inputs
+        self.record = {}
+
+    def _forward(self, items, all_rows):
+        pr, outs = self.m.forward(items, self.m_inputs)
+        owner = {s.ts: s.req.id for s in self.streams}
+        r = 0
+        for ts, toks in items:
+            for _ in toks:
+                for layer, o in enumerate(outs):
+                    self.record[(owner[ts], int(pr.meta.pos[r]), layer)] = np.asarray(o)[r]
+                r += 1
+        toks = self.token_fn(pr, outs)
+        return toks if all_rows else [toks[i] for i in pr.last]
+
+
+class OracleModelBackend:
+    def new_kv(self, layers, pages, page, hkv):
+        return [OracleArena(pages, page, hkv, D) for _ in range(layers)]
+
+    def copy_pages(self, kv, copies):
+        for c in copies:
+            for a in kv:
+                a.copy_page(c.src, c.dst)
+
+    def begin_pass(self, meta):
+        self.meta = meta
+
+    def attend_append(self, kv, layer, k, v, q, hq, window=None):
+        m = self.meta
+        kv[layer].store(m.kv_slot, k.reshape(len(m.pos), -1), v.reshape(len(m.pos), -1))
+        return kv[layer].attend(q, hq, m.pos, m.pt_off, m.pages, window=window or 0)
+
+
+def run(backend, reqs, together):
+    model = PagedModel(backend, PAGES, max_pos=4096, page=PAGE, layers=LAYERS, hkv=HKV, hq=HQ,
+                       windows=[0, 64], chunk=96)
+    eng = Recording(model, EngineConfig(decode_rows=4, busy_prefill_rows=32), token_fn=token_fn)
+    if together:
+        for r in reqs:
+            eng.submit(r)
+        eng.run_all()
+    else:
+        for r in reqs:
+            eng.submit(r)
+            eng.run_all()
+    return eng.record
+
+
+def test_concurrent_matches_solo_and_the_oracle(hip):
+    reqs = [Request(i, [(i * 37 + t) % 90 + 1 for t in range(n)], 6)
+            for i, n in enumerate([150, 17, 64, 230, 5])]
+    solo = run(hip, reqs, together=False)
+    both = run(hip, reqs, together=True)
+    orc = run(OracleModelBackend(), reqs, together=True)
+    assert set(solo) == set(both) == set(orc)
+    for key in both:
+        assert close(both[key], solo[key]).all(), key
+        assert close(both[key], orc[key]).all(), key
