@@ -51,7 +51,11 @@ int yx_sync(yx_ctx* ctx);
 /* Tuning knobs: "attn_target_waves" (waves the split-K work list aims at; 0, the
  * default, means one work item per CU), "attn_max_chunk_blocks" (most 16-key blocks per
  * work item), "attn_max_tiles" (most 8-row MFMA tiles a decode wave holds, 1-4),
- * "prefill_min_rows" (rows of one sequence from which the prefill kernel is used). */
+ * "prefill_min_rows" (rows of one sequence from which the prefill kernel is used),
+ * "attn_decode_shape" (0, the default: one-tile decode passes whose work items hold at
+ * most 64 blocks use the kernel whose waves share a queue of blocks; 1: the kernel with
+ * a fixed split of blocks over waves only). Setting an option drops cached work lists.
+ * Values are positive; 0 is accepted for attn_target_waves and attn_decode_shape. */
 int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
 
 /* Backend::new_kv (lib.rs:118; GPU ops/mod.rs:42-66): `layers` layers of `pages`

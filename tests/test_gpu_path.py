@@ -5,6 +5,8 @@ with f32 accumulation): attention outputs vs the f32 restatement of
 `LayerPass::attend` (crates/yaxus-backend-cpu/src/lib.rs:389-427) on the same f16 K/V.
 """
 
+import contextlib
+
 import numpy as np
 import pytest
 
@@ -67,9 +69,21 @@ def test_copy_pages_in_order(hip):
         _check_pages(sc, layer, list(range(8)))
 
 
+@contextlib.contextmanager
+def option(hip, key, value):
+    hip.set_option(key, value)
+    try:
+        yield
+    finally:
+        hip.set_option(key, 0)
+
+
+# attn_decode_shape: 0 = the balanced one-tile kernel where it applies (waves share a
+# queue of quads), 1 = the static-split kernel only.
+@pytest.mark.parametrize("shape", [0, 1])
 @pytest.mark.parametrize("page", [16, 128])
 @pytest.mark.parametrize("window", [0, 100])
-def test_decode_matches_oracle(hip, page, window):
+def test_decode_matches_oracle(hip, page, window, shape):
     hq, hkv = 16, 4
     sc = Scenario(hip, pages=256 if page == 16 else 48, page=page, hkv=hkv, pool_seed=11)
     lens = [1, 15, 16, 17, 300, 1000, 33, 250]
@@ -79,14 +93,16 @@ def test_decode_matches_oracle(hip, page, window):
     sc.store(pr)
     rows = len(seqs)
     q = sc.draw(rows * hq * D).reshape(rows, hq * D)
-    got = hip.attend(sc.kv, 0, q, hq, window=window)
+    with option(hip, "attn_decode_shape", shape):
+        got = hip.attend(sc.kv, 0, q, hq, window=window)
     want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
     err = np.abs(got - want).max()
     assert close(got, want).all(), f"max abs err {err}"
 
 
+@pytest.mark.parametrize("shape", [0, 1])
 @pytest.mark.parametrize("target_waves", [1, 64, 4096])
-def test_split_count_does_not_change_results(hip, target_waves):
+def test_split_count_does_not_change_results(hip, target_waves, shape):
     hq, hkv = 8, 2
     sc = Scenario(hip, pages=160, page=16, hkv=hkv, pool_seed=5)
     seqs = [sc.cache.new_seq() for _ in range(3)]
@@ -94,11 +110,8 @@ def test_split_count_does_not_change_results(hip, target_waves):
     pr = sc.run_pass([(s, 1) for s in seqs])
     sc.store(pr)
     q = sc.draw(3 * hq * D).reshape(3, hq * D)
-    hip.set_option("attn_target_waves", target_waves)
-    try:
+    with option(hip, "attn_target_waves", target_waves), option(hip, "attn_decode_shape", shape):
         got = hip.attend(sc.kv, 0, q, hq)
-    finally:
-        hip.set_option("attn_target_waves", 0)
     want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
     assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
 
@@ -153,9 +166,10 @@ def test_fused_append_attention(hip, hq, hkv, k, window):
     _check_pages(sc, 0, used)
 
 
-def test_attention_is_deterministic(hip):
-    """Chunks are merged in chunk order and each wave's blocks are fixed: two runs of
-    the same pass give the same bits."""
+@pytest.mark.parametrize("shape", [0, 1])
+def test_attention_is_deterministic(hip, shape):
+    """Chunks are merged in chunk order, and quads of blocks in quad order whichever
+    wave ran them (or each wave's blocks are fixed): two runs give the same bits."""
     hq, hkv = 16, 4
     sc = Scenario(hip, pages=800, page=16, hkv=hkv, pool_seed=8)
     seqs = [sc.cache.new_seq() for _ in range(8)]
@@ -163,8 +177,9 @@ def test_attention_is_deterministic(hip):
     pr = sc.run_pass([(s, 1) for s in seqs])
     sc.store(pr)
     q = sc.draw(8 * hq * D).reshape(8, hq * D)
-    a = hip.attend(sc.kv, 0, q, hq)
-    b = hip.attend(sc.kv, 0, q, hq)
+    with option(hip, "attn_decode_shape", shape):
+        a = hip.attend(sc.kv, 0, q, hq)
+        b = hip.attend(sc.kv, 0, q, hq)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 

@@ -121,6 +121,125 @@ struct DecodeShared {
   uint32_t last;
 };
 
+// Fused append: the group's own new rows are stored by the work item of its last
+// chunk, which holds every block they fall in (the host makes sure of that), before its
+// waves read them. Only the keys of this kv head.
+template <int kThreads>
+__device__ __forceinline__ void fused_append(const AttnItem& it, uint32_t kh, uint32_t hkv,
+                                             uint32_t bpp_shift, const float* __restrict__ knew,
+                                             const float* __restrict__ vnew,
+                                             const uint32_t* __restrict__ kv_slot, _Float16* kw,
+                                             _Float16* vw) {
+  const uint32_t page_size = 16u << bpp_shift;
+  for (uint32_t i = threadIdx.x; i < it.nrows * 32; i += kThreads) {
+    const uint32_t row = it.r0 + i / 32, ch = (i / 2) % 16;
+    const bool is_k = (i & 1) == 0;
+    const float* src = (is_k ? knew : vnew) + (static_cast<size_t>(row) * hkv + kh) * kD + ch * 8;
+    const uint32_t slot = kv_slot[row];
+    const uint32_t off = slot & (page_size - 1);
+    const size_t region = (static_cast<size_t>(slot >> (bpp_shift + 4)) * hkv + kh) * page_size * kD;
+    _Float16* dst = is_k ? kw + region + k_offset(off, ch) : vw + region + off * kD + ch * 8;
+    const float4 a = *reinterpret_cast<const float4*>(src);
+    const float4 b = *reinterpret_cast<const float4*>(src + 4);
+    *reinterpret_cast<half8*>(dst) =
+        half8{static_cast<_Float16>(a.x), static_cast<_Float16>(a.y), static_cast<_Float16>(a.z),
+              static_cast<_Float16>(a.w), static_cast<_Float16>(b.x), static_cast<_Float16>(b.y),
+              static_cast<_Float16>(b.z), static_cast<_Float16>(b.w)};
+  }
+  // Stores complete, then the workgroup barrier orders them before every wave's loads
+  // (the waves of a workgroup share one CU and its L1).
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
+// Hands a workgroup's result for its logical rows on: straight to `out` when the item
+// is its group's only chunk, else to the item's partial slot, after which the last item
+// of the group to arrive merges all partials in chunk order (so the result does not
+// depend on arrival order). value(lr, qi, mt, lt, o) gives the workgroup's maximum, sum
+// and unnormalised O (dims 4qi..4qi+3) of logical row lr.
+template <int kThreads, int kRows, typename Value>
+__device__ __forceinline__ void finish_item(const AttnItem& it, uint32_t kh, uint32_t G, uint32_t hq,
+                                            uint32_t hkv, uint32_t nlog, float* __restrict__ out,
+                                            float* __restrict__ part_o, float2* __restrict__ part_ml,
+                                            uint32_t* __restrict__ counters, uint32_t part_o_bytes,
+                                            uint32_t part_ml_bytes, uint32_t& last, Value value) {
+  const size_t qd = static_cast<size_t>(hq) * kD;
+  const uint32_t rows_per_slot = kRows;
+  const size_t slot = (static_cast<size_t>(it.part_base) + it.chunk) * hkv + kh;
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(part_o, part_o_bytes);
+  const __amdgpu_buffer_rsrc_t rml = make_rsrc(part_ml, part_ml_bytes);
+  constexpr int kPer = (kRows * 32 + kThreads - 1) / kThreads;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t idx = threadIdx.x + k * kThreads;
+    const uint32_t lr = idx >> 5, qi = idx & 31;
+    if (lr >= nlog || lr >= kRows) continue;
+    float mt, lt;
+    float4 o;
+    value(lr, qi, mt, lt, o);
+    if (it.nch == 1) {
+      const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
+      const float inv = 1.0f / lt;
+      *reinterpret_cast<float4*>(out + rr * qd + h * kD + qi * 4) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+    } else {
+      const size_t e = slot * rows_per_slot + lr;
+      st4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4), o);
+      if (qi == 0) st2_coherent(rml, static_cast<uint32_t>(e * 8), float2{mt, lt});
+    }
+  }
+  if (it.nch == 1) return;
+
+  // The last work item of this (group, kv head) to arrive merges all of them.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  uint32_t* cnt = counters + static_cast<size_t>(it.counter) * hkv + kh;
+  if (threadIdx.x == 0) {
+    const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = arrived == it.nch - 1;
+    if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+
+  // Each thread merges one (row, 4 dims) over the chunks in chunk order, with a
+  // running maximum; the loads of 8 chunks are in flight at a time.
+  const size_t base0 = static_cast<size_t>(it.part_base) * hkv + kh;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t idx = threadIdx.x + k * kThreads;
+    const uint32_t lr = idx >> 5, qi = idx & 31;
+    if (lr >= nlog || lr >= kRows) continue;
+    float mt = -INFINITY, lt = 0.0f;
+    float4 o = {0, 0, 0, 0};
+    for (uint32_t c0 = 0; c0 < it.nch; c0 += 8) {
+      float2 ml[8];
+      float4 po[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t ch = min(c0 + j, it.nch - 1);
+        const size_t e = (base0 + static_cast<size_t>(ch) * hkv) * rows_per_slot + lr;
+        ml[j] = ld2_coherent(rml, static_cast<uint32_t>(e * 8));
+        po[j] = ld4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (c0 + j >= it.nch || !(ml[j].y > 0.0f)) continue;  // past the end, or empty
+        const float mn = fmaxf(mt, ml[j].x);
+        const float r = __builtin_amdgcn_exp2f(mt - mn), wt = __builtin_amdgcn_exp2f(ml[j].x - mn);
+        lt = lt * r + ml[j].y * wt;
+        o.x = o.x * r + po[j].x * wt;
+        o.y = o.y * r + po[j].y * wt;
+        o.z = o.z * r + po[j].z * wt;
+        o.w = o.w * r + po[j].w * wt;
+        mt = mn;
+      }
+    }
+    const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
+    const float inv = 1.0f / lt;
+    *reinterpret_cast<float4*>(out + rr * qd + h * kD + qi * 4) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+  }
+}
+
 template <int NT, int kWaves = DecodeWaves<NT>::value>
 __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
     const AttnItem* __restrict__ items, const uint32_t* __restrict__ pos,
@@ -141,31 +260,8 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
   const uint32_t G = hq / hkv;
   const uint32_t nlog = it.nrows * G;  // logical rows in the group
 
-  // Fused append (knew != nullptr): the group's own new rows are stored by the work
-  // item of its last chunk, which holds every block they fall in (the host makes
-  // sure of that), before its waves read them. Only the keys of this kv head.
-  if (knew != nullptr && it.chunk == it.nch - 1) {
-    const uint32_t page_size = 16u << bpp_shift;
-    for (uint32_t i = threadIdx.x; i < it.nrows * 32; i += 64 * kWaves) {
-      const uint32_t row = it.r0 + i / 32, ch = (i / 2) % 16;
-      const bool is_k = (i & 1) == 0;
-      const float* src = (is_k ? knew : vnew) + (static_cast<size_t>(row) * hkv + kh) * kD + ch * 8;
-      const uint32_t slot = kv_slot[row];
-      const uint32_t off = slot & (page_size - 1);
-      const size_t region = (static_cast<size_t>(slot >> (bpp_shift + 4)) * hkv + kh) * page_size * kD;
-      _Float16* dst = is_k ? kw + region + k_offset(off, ch) : vw + region + off * kD + ch * 8;
-      const float4 a = *reinterpret_cast<const float4*>(src);
-      const float4 b = *reinterpret_cast<const float4*>(src + 4);
-      *reinterpret_cast<half8*>(dst) =
-          half8{static_cast<_Float16>(a.x), static_cast<_Float16>(a.y), static_cast<_Float16>(a.z),
-                static_cast<_Float16>(a.w), static_cast<_Float16>(b.x), static_cast<_Float16>(b.y),
-                static_cast<_Float16>(b.z), static_cast<_Float16>(b.w)};
-    }
-    // Stores complete, then the workgroup barrier orders them before every wave's loads
-    // (the waves of a workgroup share one CU and its L1).
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  }
+  if (knew != nullptr && it.chunk == it.nch - 1)
+    fused_append<64 * kWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
 
   // This wave's share of the item's blocks, [wb0, wb1), in whole quads of blocks (a
   // static split: the result does not depend on timing); at most 64 blocks per wave,
@@ -345,22 +441,14 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
   __syncthreads();
 
   // Merge the waves: thread -> (row, 4 dims); NT*8 rows x 32 quads = NT * 256 values.
-  const size_t qd = static_cast<size_t>(hq) * kD;
-  const uint32_t rows_per_slot = NT * 8;
-  const size_t slot = (static_cast<size_t>(it.part_base) + it.chunk) * hkv + kh;
-  const __amdgpu_buffer_rsrc_t ro = make_rsrc(part_o, part_o_bytes);
-  const __amdgpu_buffer_rsrc_t rml = make_rsrc(part_ml, part_ml_bytes);
-  constexpr int kPer = (NT * 256 + 64 * kWaves - 1) / (64 * kWaves);
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const uint32_t idx = threadIdx.x + k * 64 * kWaves;
-    const uint32_t lr = idx >> 5, qi = idx & 31;
-    if (lr >= nlog || lr >= NT * 8) continue;
-    float mt = -INFINITY;
+  finish_item<64 * kWaves, NT * 8>(it, kh, G, hq, hkv, nlog, out, part_o, part_ml, counters,
+                                   part_o_bytes, part_ml_bytes, sh.last,
+                                   [&](uint32_t lr, uint32_t qi, float& mt, float& lt, float4& o) {
+    mt = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) mt = fmaxf(mt, sh.m[w][lr]);
-    float lt = 0.0f;
-    float4 o = {0, 0, 0, 0};
+    lt = 0.0f;
+    o = float4{0, 0, 0, 0};
     if (mt != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
@@ -373,67 +461,242 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
         o.w += ow.w * wt;
       }
     }
-    if (it.nch == 1) {
-      const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
-      const float inv = 1.0f / lt;
-      *reinterpret_cast<float4*>(out + rr * qd + h * kD + qi * 4) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
-    } else {
-      const size_t e = slot * rows_per_slot + lr;
-      st4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4), o);
-      if (qi == 0) st2_coherent(rml, static_cast<uint32_t>(e * 8), float2{mt, lt});
+  });
+}
+
+
+// Balanced one-tile decode: the waves of a workgroup take the item's quads of blocks
+// from a queue in LDS as they finish the previous one, so a wave whose loads come back
+// late takes fewer quads instead of holding up the workgroup. Each quad's softmax state
+// starts afresh and goes to its own LDS slot, and the slots are merged in quad order,
+// so the result does not depend on which wave ran which quad. At most kBalQuads quads
+// (64 blocks) per item; block loads go through buffer resources whose size is zero for
+// blocks past the item's end, so the prefetch of a quad that does not exist reads
+// nothing. A wave keeps two blocks (16 KiB) in flight: measured against two pairs, as
+// fast or faster, with fewer registers.
+static constexpr int kBalWaves = 8;
+static constexpr uint32_t kBalQuads = 16;
+static constexpr int kNontemporal = 2;  // nt
+
+struct BalancedShared {
+  float m[kBalQuads][8];
+  float l[kBalQuads][8];
+  float4 o[kBalQuads][8][kD / 4];
+  uint32_t next;
+  uint32_t last;
+};
+
+__device__ __forceinline__ void load_block_buf(BlockRegs& r, const _Float16* kblk, const _Float16* vblk,
+                                               bool valid, int lane) {
+  const int c = lane & 15, g = lane >> 4;
+  const int bytes = valid ? 2048 * 2 : 0;
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(kblk), 0, bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(vblk), 0, bytes, 0x00020000);
+#pragma unroll
+  for (int p = 0; p < 4; ++p)  // [p][key c][g] in 16-byte units
+    r.k[p] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, ((c * 4 + g) + p * 64) * 16, 0, kNontemporal));
+#pragma unroll
+  for (int i = 0; i < 4; ++i)  // key 4g + i, dims c*8..c*8+7
+    r.v[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, ((4 * g + i) * kD + c * 8) * 2, 0, kNontemporal));
+}
+
+__global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
+    const AttnItem* __restrict__ items, const uint32_t* pos,
+    const uint32_t* __restrict__ pages, const _Float16* kc, const _Float16* vc,
+    const float* q, float* __restrict__ out,
+    float* __restrict__ part_o, float2* __restrict__ part_ml, uint32_t* __restrict__ counters,
+    const float* __restrict__ knew, const float* __restrict__ vnew,
+    const uint32_t* __restrict__ kv_slot, _Float16* kw, _Float16* vw,  // kw/vw alias kc/vc
+    uint32_t part_o_bytes, uint32_t part_ml_bytes, uint32_t hq, uint32_t hkv,
+    uint32_t bpp_shift, uint32_t window, float scale_log2) {
+  __shared__ BalancedShared sh;
+  const AttnItem it = items[blockIdx.x];
+  const uint32_t kh = blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, g = lane >> 4;
+  const bool lo_half = c >= 8;
+  const uint32_t G = hq / hkv;
+  const uint32_t nlog = it.nrows * G;  // logical rows in the group (at most 8)
+
+  if (threadIdx.x == 0) sh.next = kBalWaves;  // quads 0..W-1 go to waves 0..W-1
+  if (knew != nullptr && it.chunk == it.nch - 1)
+    fused_append<64 * kBalWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
+  else
+    __syncthreads();
+
+  const uint32_t nall = it.blk1 - it.blk0;  // at most 4 * kBalQuads (host-checked)
+  const uint32_t nq = (nall + 3) / 4;
+  const uint32_t bpp_mask = (1u << bpp_shift) - 1u;
+  const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;
+  const uint32_t* pt = pages + it.pt_off;
+  int pid = 0;  // page id of block blk0 + lane
+  if (static_cast<uint32_t>(lane) < nall) pid = static_cast<int>(pt[(it.blk0 + lane) >> bpp_shift]);
+  const int key_end = static_cast<int>(it.blk1 * 16);
+
+  // Two register sets of one block each, used in turn: the loads of one are in flight
+  // while the other is computed.
+  BlockRegs s0, s1;
+  // Loads block b (relative to blk0; wave-uniform) into r.
+  auto load_set = [&](BlockRegs& r, uint32_t b) {
+    const bool valid = b < nall;
+    const uint32_t page = static_cast<uint32_t>(__builtin_amdgcn_readlane(pid, static_cast<int>(valid ? b : 0)));
+    const size_t o = (static_cast<size_t>(page) * hkv + kh) * head_stride +
+                     static_cast<size_t>((it.blk0 + b) & bpp_mask) * 16 * kD;
+    load_block_buf(r, kc + o, vc + o, valid, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // This lane's column: its row's position and key window; q is read before the first
+  // blocks (so that waiting for it does not wait for them) and split into the hi or lo
+  // part after.
+  // (Unconditional loads, clamped to a valid row: a branch around them would make the
+  // compiler wait for every load before the first block's page id.)
+  const bool has_row = (c & 7) < nlog;
+  const uint32_t lr0 = has_row ? (c & 7) : 0;
+  const uint32_t rr0 = it.r0 + lr0 / G, h0 = kh * G + lr0 % G;
+  const int p0 = static_cast<int>(pos[rr0]);
+  const int rpos = has_row ? p0 : -1;
+  const int rlo = (window > 0 && p0 + 1 > static_cast<int>(window)) ? p0 + 1 - static_cast<int>(window) : 0;
+  float4 qraw[8];
+  {
+    const float* qp = q + (static_cast<size_t>(rr0) * hq + h0) * kD + g * 8;
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      qraw[2 * pp] = *reinterpret_cast<const float4*>(qp + pp * 32);
+      qraw[2 * pp + 1] = *reinterpret_cast<const float4*>(qp + pp * 32 + 4);
     }
   }
-  if (it.nch == 1) return;
-
-  // The last work item of this (group, kv head) to arrive merges all of them.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  uint32_t* cnt = counters + static_cast<size_t>(it.counter) * hkv + kh;
-  if (threadIdx.x == 0) {
-    const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sh.last = arrived == it.nch - 1;
-    if (sh.last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Issue them here, ahead of the blocks (q and pos are not declared __restrict__ and the
+  // empty asm may write memory, so the compiler cannot sink the loads to their use; the
+  // scheduling barrier keeps the scheduler from doing so).
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t qc = static_cast<uint32_t>(wave);  // this wave's current quad
+  load_set(s0, 4 * qc);
+  load_set(s1, 4 * qc + 1);
+  half8 qb[4];
+#pragma unroll
+  for (int pp = 0; pp < 4; ++pp) {
+    const float4 a = qraw[2 * pp], b = qraw[2 * pp + 1];
+    float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = has_row ? x[e] : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const _Float16 hi = static_cast<_Float16>(x[e]);
+      qb[pp][e] = lo_half ? static_cast<_Float16>(x[e] - static_cast<float>(hi)) : hi;
+    }
   }
-  __syncthreads();
-  if (!sh.last) return;
 
-  // Each thread merges one (row, 4 dims) over the chunks in chunk order, with a
-  // running maximum; the loads of 8 chunks are in flight at a time.
-  const size_t base0 = static_cast<size_t>(it.part_base) * hkv + kh;
+  float m, l;
+  floatx4 acc[8];
+  auto process_set = [&](const BlockRegs& r, uint32_t b) {
+    const int kb0 = static_cast<int>((it.blk0 + b) * 16) + 4 * g;
+    float x[4];
+    float bmax = -INFINITY;
+    floatx4 sc = {0, 0, 0, 0};
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const uint32_t idx = threadIdx.x + k * 64 * kWaves;
-    const uint32_t lr = idx >> 5, qi = idx & 31;
-    if (lr >= nlog || lr >= NT * 8) continue;
-    float mt = -INFINITY, lt = 0.0f;
-    float4 o = {0, 0, 0, 0};
-    for (uint32_t c0 = 0; c0 < it.nch; c0 += 8) {
-      float2 ml[8];
-      float4 po[8];
+    for (int p = 0; p < 4; ++p) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.k[p], qb[p], sc, 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t ch = min(c0 + j, it.nch - 1);
-        const size_t e = (base0 + static_cast<size_t>(ch) * hkv) * rows_per_slot + lr;
-        ml[j] = ld2_coherent(rml, static_cast<uint32_t>(e * 8));
-        po[j] = ld4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4));
+    for (int i = 0; i < 4; ++i) {
+      const float full = sc[i] + xor8(sc[i]);
+      const int kp = kb0 + i;
+      const bool ok = (kp >= rlo) & (kp <= rpos) & (kp < key_end);
+      x[i] = ok ? full * scale_log2 : -INFINITY;
+      bmax = fmaxf(bmax, x[i]);
+    }
+    bmax = fmaxf(bmax, xor16(bmax));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+    const float mn = fmaxf(m, bmax);
+    const bool live = mn != -INFINITY;
+    float pr[4], rs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pr[i] = live ? __builtin_amdgcn_exp2f(x[i] - mn) : 0.0f;
+      rs += pr[i];
+    }
+    rs += xor16(rs);
+    rs += __shfl_xor(rs, 32);
+    if (__builtin_amdgcn_ballot_w64(mn != m)) {
+      const float corr = live ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
+      l *= corr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] *= corr;
+    }
+    l += rs;
+    m = mn;
+    // PV (16x16x16): element e of the P operand is key 4g + e, as in the V operand.
+    half4 pb;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const _Float16 hi = static_cast<_Float16>(pr[e]);
+      pb[e] = lo_half ? static_cast<_Float16>(pr[e] - static_cast<float>(hi)) : hi;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const half4 a = {r.v[0][j], r.v[1][j], r.v[2][j], r.v[3][j]};
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, acc[j], 0, 0, 0);
+    }
+  };
+
+  while (qc < nq) {
+    uint32_t taken = 0;
+    if (lane == 0) taken = __hip_atomic_fetch_add(&sh.next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const uint32_t qn = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(taken)));
+    m = -INFINITY;
+    l = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = floatx4{0, 0, 0, 0};
+    // The quad's four blocks in turn; each load goes two blocks ahead, into the next
+    // quad for the last two.
+    process_set(s0, 4 * qc);
+    load_set(s0, 4 * qc + 2);
+    process_set(s1, 4 * qc + 1);
+    load_set(s1, 4 * qc + 3);
+    process_set(s0, 4 * qc + 2);
+    load_set(s0, 4 * qn);
+    process_set(s1, 4 * qc + 3);
+    load_set(s1, 4 * qn + 1);
+    // Join the hi and lo columns and store the quad's state in its slot.
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[j][i] += xor8(acc[j][i]);
+    if (c < 8) {
+      if (g == 0) {
+        sh.m[qc][c] = m;
+        sh.l[qc][c] = l;
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (c0 + j >= it.nch || !(ml[j].y > 0.0f)) continue;  // past the end, or empty
-        const float mn = fmaxf(mt, ml[j].x);
-        const float r = __builtin_amdgcn_exp2f(mt - mn), wt = __builtin_amdgcn_exp2f(ml[j].x - mn);
-        lt = lt * r + ml[j].y * wt;
-        o.x = o.x * r + po[j].x * wt;
-        o.y = o.y * r + po[j].y * wt;
-        o.z = o.z * r + po[j].z * wt;
-        o.w = o.w * r + po[j].w * wt;
-        mt = mn;
+      for (int i = 0; i < 4; ++i) {
+        sh.o[qc][c][g * 8 + i * 2] = float4{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
+        sh.o[qc][c][g * 8 + i * 2 + 1] = float4{acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
       }
     }
-    const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
-    const float inv = 1.0f / lt;
-    *reinterpret_cast<float4*>(out + rr * qd + h * kD + qi * 4) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+    qc = qn;
   }
+  __syncthreads();
+
+  finish_item<64 * kBalWaves, 8>(it, kh, G, hq, hkv, nlog, out, part_o, part_ml, counters,
+                                 part_o_bytes, part_ml_bytes, sh.last,
+                                 [&](uint32_t lr, uint32_t qi, float& mt, float& lt, float4& o) {
+    mt = -INFINITY;
+    for (uint32_t k = 0; k < nq; ++k) mt = fmaxf(mt, sh.m[k][lr]);
+    lt = 0.0f;
+    o = float4{0, 0, 0, 0};
+    if (mt == -INFINITY) return;
+    for (uint32_t k = 0; k < nq; ++k) {
+      const float wt = __builtin_amdgcn_exp2f(sh.m[k][lr] - mt);  // 0 for an empty quad
+      lt += sh.l[k][lr] * wt;
+      const float4 ow = sh.o[k][lr][qi];
+      o.x += ow.x * wt;
+      o.y += ow.y * wt;
+      o.z += ow.z * wt;
+      o.w += ow.w * wt;
+    }
+  });
 }
 
 }  // namespace yx

@@ -110,6 +110,7 @@ struct AttnPlan {
   bool prefill = false;  // MFMA tiles over LDS (many rows per sequence) vs split-K decode
   std::vector<yx::PrefillItem> pitems;
   int nt = 1;
+  bool balanced = false;  // one tile, items of at most kBalQuads quads: waves share a queue
   std::vector<yx::AttnItem> items;
   DevBuf d_items;
   bool fusable = false;  // the append can run inside the attention kernel
@@ -169,6 +170,7 @@ struct yx_ctx {
   long max_chunk_blocks = 1 << 20;
   long prefill_min_rows = 32;
   long max_tiles = 4;
+  long decode_shape = 0;  // 0: balanced one-tile kernel where it applies, 1: static split only
   bool profiling = false;
   Profile prof[3];
   bool capturing = false;
@@ -346,6 +348,9 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
       if (w.blk0 * 16 > pmin) plan.fusable = false;
     }
   }
+  plan.balanced = nt == 1 && c->decode_shape == 0;
+  for (const yx::AttnItem& w : plan.items)
+    if (w.blk1 - w.blk0 > 4 * yx::kBalQuads) plan.balanced = false;
   plan.slots = slot;
   plan.counters = subs.size();
   if (plan.items.size() > 0x7fffffff) return fail(YX_ERR_UNSUPPORTED, "too many work items");
@@ -424,7 +429,12 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
                      kv->k[layer], kv->v[layer], q, out, po, pml, cnt, knew, vnew,                 \
                      static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],       \
                      po_bytes, pml_bytes, H, HK, P, W, scale_log2)
-  switch (plan->nt) {
+  if (plan->balanced) {
+    hipLaunchKernelGGL(yx::paged_attn_decode_balanced, grid, dim3(64 * yx::kBalWaves), 0, c->stream,
+                       items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml, cnt, knew, vnew,
+                       static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],
+                       po_bytes, pml_bytes, H, HK, P, W, scale_log2);
+  } else switch (plan->nt) {
     case 1: YX_LAUNCH_DECODE(1); break;
     case 2: YX_LAUNCH_DECODE(2); break;
     case 3: YX_LAUNCH_DECODE(3); break;
@@ -518,12 +528,16 @@ int yx_sync(yx_ctx* c) {
 
 int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
   if (!c || !key) return fail(YX_ERR_INVALID, "null argument");
-  if (value < 0 || (value == 0 && std::strcmp(key, "attn_target_waves")))
-    return fail(YX_ERR_INVALID, "option values are positive (attn_target_waves: 0 = automatic)");
+  if (value < 0 || (value == 0 && std::strcmp(key, "attn_target_waves") &&
+                    std::strcmp(key, "attn_decode_shape")))
+    return fail(YX_ERR_INVALID,
+                "option values are positive (attn_target_waves, attn_decode_shape: 0 = automatic)");
   if (!std::strcmp(key, "attn_target_waves"))
     c->target_waves = value;
   else if (!std::strcmp(key, "attn_max_tiles"))
     c->max_tiles = std::min<long>(value, 4);
+  else if (!std::strcmp(key, "attn_decode_shape"))
+    c->decode_shape = std::min<long>(value, 1);
   else if (!std::strcmp(key, "prefill_min_rows"))
     c->prefill_min_rows = value;
   else if (!std::strcmp(key, "attn_max_chunk_blocks"))
