@@ -60,9 +60,40 @@ static constexpr uint32_t kMaxChunks = 256;
 __device__ __forceinline__ float xor8(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
 }
-// Lane l reads lane l^16 (swizzle, bit-mask mode: and 0x1f, or 0, xor 0x10).
-__device__ __forceinline__ float xor16(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
+
+// Reductions over lanes l and l^16, or l and l^32, for every lane: the gfx950 permlane
+// swaps exchange rows of 16 (or halves of 32) lanes between two registers in the VALU,
+// without the LDS round trip of a swizzle or bpermute. With both registers holding the
+// same value, each lane ends up with its own value in one and its partner's in the
+// other; max and + are commutative, so both lanes of a pair get the same bits. Written
+// as inline asm: the compiler's builtin for the swap treats the two results of a swap
+// of equal inputs as equal, which they are not across lanes. The s_nop covers the
+// wait states a swap needs after a VALU write of its operands.
+__device__ __forceinline__ void permlane16_swap(float& a, float& b) {
+  __asm__("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane32_swap(float& a, float& b) {
+  __asm__("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float max_xor16(float x) {
+  float a = x, b = x;
+  permlane16_swap(a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  float a = x, b = x;
+  permlane32_swap(a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  float a = x, b = x;
+  permlane16_swap(a, b);
+  return a + b;
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  float a = x, b = x;
+  permlane32_swap(a, b);
+  return a + b;
 }
 
 // Write-through 16-byte store / coherent load of split-K partials through a buffer
@@ -358,8 +389,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
           bmax = fmaxf(bmax, x[h * 4 + i]);
         }
       }
-      bmax = fmaxf(bmax, xor16(bmax));
-      bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+      bmax = max_xor32(max_xor16(bmax));
       const float mn = fmaxf(m[t], bmax);
       const bool live = mn != -INFINITY;
       float pr[8], rs = 0.0f;
@@ -368,8 +398,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
         pr[i] = live ? __builtin_amdgcn_exp2f(x[i] - mn) : 0.0f;
         rs += pr[i];
       }
-      rs += xor16(rs);
-      rs += __shfl_xor(rs, 32);
+      rs = sum_xor32(sum_xor16(rs));
       // Rescale only when some column's maximum moved (wave-uniform test).
       if (__builtin_amdgcn_ballot_w64(mn != m[t])) {
         const float corr = live ? __builtin_amdgcn_exp2f(m[t] - mn) : 1.0f;
@@ -607,8 +636,7 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
       x[i] = ok ? full * scale_log2 : -INFINITY;
       bmax = fmaxf(bmax, x[i]);
     }
-    bmax = fmaxf(bmax, xor16(bmax));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+    bmax = max_xor32(max_xor16(bmax));
     const float mn = fmaxf(m, bmax);
     const bool live = mn != -INFINITY;
     float pr[4], rs = 0.0f;
@@ -617,8 +645,7 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
       pr[i] = live ? __builtin_amdgcn_exp2f(x[i] - mn) : 0.0f;
       rs += pr[i];
     }
-    rs += xor16(rs);
-    rs += __shfl_xor(rs, 32);
+    rs = sum_xor32(sum_xor16(rs));
     if (__builtin_amdgcn_ballot_w64(mn != m)) {
       const float corr = live ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
       l *= corr;

@@ -9,7 +9,7 @@
 // blocks of 16 (two buffers: stage s+1 is fetched from HBM into registers while stage s
 // is computed, then written to the other buffer), and every wave reads them there:
 //   S^T[key][row] = K . Q^T      8 x v_mfma_f32_16x16x32_f16 per tile (q as hi + lo f16)
-//   online softmax per column, once per 32 keys (xor-16 swizzle, 32-lane shuffle);
+//   online softmax per column, once per 32 keys (permlane swaps across lane halves);
 //   the accumulator is rescaled only when a column's maximum moved
 //   O^T += V^T P^T               16 x v_mfma_f32_16x16x32_f16 per tile and 32 keys (P hi + lo)
 // q and P each go in as a binary16 hi part plus a lo part, two products into one
@@ -39,19 +39,37 @@ static constexpr int kPrefillTiles = 2;  // MFMA tiles (16 logical rows) per wav
 static constexpr int kPrefillRows = kPrefillWaves * kPrefillTiles * 16;  // logical rows per item
 
 static constexpr int kStageBlocks = 2;  // 16-key blocks per LDS stage (32 keys, 16 KiB of K+V)
+static constexpr int kRing = 6;         // LDS stages: kRing - 1 in flight while one is computed
+
+// One 16-byte piece per lane from global memory straight into LDS (no registers): lane
+// i's piece lands at LDS byte address `lds` + 16 i. M0 holds the wave's LDS base for
+// the instruction and is restored afterwards. The load counts in vmcnt like any other;
+// callers wait for it explicitly (the compiler does not know about it).
+__device__ __forceinline__ void load_to_lds16(const void* src, uint32_t lds) {
+  uint32_t saved;
+  __asm__ volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(lds)
+      : "memory");
+}
 
 __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
-    const PrefillItem* __restrict__ items, const uint32_t* __restrict__ pos,
+    const PrefillItem* __restrict__ items, const uint32_t* pos,
     const uint32_t* __restrict__ pages, const _Float16* __restrict__ kc,
-    const _Float16* __restrict__ vc, const float* __restrict__ q, float* __restrict__ out,
+    const _Float16* __restrict__ vc, const float* q, float* __restrict__ out,
     uint32_t hq, uint32_t hkv, uint32_t bpp_shift, uint32_t window, float scale_log2) {
   constexpr int NT = kPrefillTiles, SB = kStageBlocks;
-  __shared__ half8 kbuf[2][SB * 256];  // a stage of K blocks (4 KiB each), [p][g][key]
-  __shared__ half8 vbuf[2][SB * 256];  // and of V
+  // A ring of stages; each holds SB blocks of K as [p][g][key] (4 KiB each) and then SB
+  // blocks of V as [key][128] (4 KiB each).
+  __shared__ half8 ring[kRing][2 * SB * 256];
   const PrefillItem it = items[blockIdx.x];
   const uint32_t kh = blockIdx.y;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int c = lane & 15, g = lane >> 4;
   const uint32_t G = hq / hkv;
   const uint32_t nlog = it.nrows * G;
@@ -59,51 +77,70 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
   const uint32_t bpp_mask = (1u << bpp_shift) - 1u;
   const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;
   const uint32_t* pt = pages + it.pt_off;
-  auto block_ptr = [&](uint32_t b, const _Float16* base) {
-    b = b < it.blk1 ? b : it.blk1 - 1;  // past the end: re-read the last block (masked)
+  // Each wave moves a quarter of a stage: wave w takes block w / 2 of the stage, its K
+  // (w even) or V (w odd), as four 1 KiB rows. K row p is read transposed ([p][key][g]
+  // in the arena, [p][g][key] in LDS): lane l fetches key l % 16, dims group l / 16.
+  const uint32_t my_blk = static_cast<uint32_t>(wave >> 1);
+  const bool my_v = (wave & 1) != 0;
+  const uint32_t lane_src = my_v ? static_cast<uint32_t>(lane) * 16u
+                                 : static_cast<uint32_t>((lane & 15) * 4 + (lane >> 4)) * 16u;
+  const char* my_arena = reinterpret_cast<const char*>(my_v ? vc : kc);
+  const uint32_t ring_base = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) half8*)&ring[0][0]));
+  auto issue = [&](uint32_t st, uint32_t slot) {  // stage st into ring slot `slot`
+    uint32_t b = it.blk0 + st * SB + my_blk;
+    b = b < it.blk1 ? b : it.blk1 - 1;  // past the end: re-read the last block (unused)
     const uint32_t page = pt[b >> bpp_shift];
-    return reinterpret_cast<const half8*>(base + (static_cast<size_t>(page) * hkv + kh) * head_stride +
-                                          static_cast<size_t>(b & bpp_mask) * 16 * kD);
-  };
-  half8 kreg[SB], vreg[SB];
-  auto fetch = [&](uint32_t b0) {
+    const char* blk = my_arena + ((static_cast<size_t>(page) * hkv + kh) * head_stride +
+                                  static_cast<size_t>(b & bpp_mask) * 16 * kD) * 2;
+    const uint32_t dst = ring_base + slot * (2 * SB * 256 * 16) +
+                         (my_v ? SB * 4096u : 0u) + my_blk * 4096u;
 #pragma unroll
-    for (int i = 0; i < SB; ++i) {
-      kreg[i] = __builtin_nontemporal_load(block_ptr(b0 + i, kc) + tid);
-      vreg[i] = __builtin_nontemporal_load(block_ptr(b0 + i, vc) + tid);
-    }
+    for (int r = 0; r < 4; ++r) load_to_lds16(blk + r * 1024 + lane_src, dst + r * 1024);
   };
-  fetch(it.blk0);  // the first stage is in flight while q is set up
-
-  half8 qh[NT][4], ql[NT][4];  // q as binary16 hi + lo parts
+  // q and pos are read first, unconditionally (rows past the tile read row 0 and are
+  // zeroed), so that waiting for them does not wait for the K/V stages issued after.
+  // q and pos are not declared __restrict__ and the empty asm may write memory, so the
+  // compiler cannot sink these loads below the stage loads.
+  float4 qraw[NT][8];
   int rpos[NT], rlo[NT];
+  bool has[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const uint32_t lr = (wave * NT + t) * 16 + c;
-    rpos[t] = -1;
-    rlo[t] = 0;
-    if (lr < nlog) {
-      const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
-      const int p = static_cast<int>(pos[rr]);
-      rpos[t] = p;
-      rlo[t] = (window > 0 && p + 1 > static_cast<int>(window)) ? p + 1 - static_cast<int>(window) : 0;
-      const float* qp = q + (static_cast<size_t>(rr) * hq + h) * kD + g * 8;
+    has[t] = lr < nlog;
+    const uint32_t lrc = has[t] ? lr : 0;
+    const uint32_t rr = it.r0 + lrc / G, h = kh * G + lrc % G;
+    const int p = static_cast<int>(pos[rr]);
+    rpos[t] = has[t] ? p : -1;
+    rlo[t] = (window > 0 && p + 1 > static_cast<int>(window)) ? p + 1 - static_cast<int>(window) : 0;
+    const float* qp = q + (static_cast<size_t>(rr) * hq + h) * kD + g * 8;
 #pragma unroll
-      for (int pp = 0; pp < 4; ++pp) {
-        const float4 a = *reinterpret_cast<const float4*>(qp + pp * 32);
-        const float4 b = *reinterpret_cast<const float4*>(qp + pp * 32 + 4);
-        const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          qh[t][pp][e] = static_cast<_Float16>(x[e]);
-          ql[t][pp][e] = static_cast<_Float16>(x[e] - static_cast<float>(qh[t][pp][e]));
-        }
-      }
-    } else {
-#pragma unroll
-      for (int pp = 0; pp < 4; ++pp) qh[t][pp] = ql[t][pp] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+    for (int pp = 0; pp < 4; ++pp) {
+      qraw[t][2 * pp] = *reinterpret_cast<const float4*>(qp + pp * 32);
+      qraw[t][2 * pp + 1] = *reinterpret_cast<const float4*>(qp + pp * 32 + 4);
     }
   }
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t nst = (it.blk1 - it.blk0 + SB - 1) / SB;  // stages
+#pragma unroll
+  for (int j = 0; j < kRing - 1; ++j) issue(j, j);
+
+  half8 qh[NT][4], ql[NT][4];  // q as binary16 hi + lo parts
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      const float4 a = qraw[t][2 * pp], b = qraw[t][2 * pp + 1];
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = has[t] ? x[e] : 0.0f;
+        qh[t][pp][e] = static_cast<_Float16>(v);
+        ql[t][pp][e] = static_cast<_Float16>(v - static_cast<float>(qh[t][pp][e]));
+      }
+    }
   // Uniform limits: per tile the last row's position, the first row's position and the
   // largest window start; per wave the key range any of its rows sees.
   int tmax[NT], tmin[NT], tlo[NT];
@@ -136,18 +173,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
   }
   const int key_end = static_cast<int>(it.blk1 * 16);
 
-  for (uint32_t s0 = it.blk0; s0 < it.blk1; s0 += SB) {
-    const int buf = ((s0 - it.blk0) / SB) & 1;
-    // K goes to LDS as [p][g][key] (the arena's [p][key][g] transposed within each 1 KiB
-    // row group), so that each wave's operand reads are 64 consecutive 16-byte pieces.
-    const int kdst = (tid & ~63) | ((tid & 3) << 4) | ((tid >> 2) & 15);
-#pragma unroll
-    for (int i = 0; i < SB; ++i) {
-      kbuf[buf][i * 256 + kdst] = kreg[i];
-      vbuf[buf][i * 256 + tid] = vreg[i];
-    }
-    __syncthreads();
-    if (s0 + SB < it.blk1) fetch(s0 + SB);  // the next stage streams in during this one
+  auto compute = [&](const half8* kbuf, const half8* vbuf, uint32_t s0) {
     // Two blocks (32 keys) per softmax update; PV as 16x16x32 products over both.
 #pragma unroll
     for (int pr2 = 0; pr2 < SB / 2; ++pr2) {
@@ -158,9 +184,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
       for (int h = 0; h < 2; ++h) {
         const int base = (2 * pr2 + h) * 256;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) kk[h][p] = kbuf[buf][base + p * 64 + lane];
+        for (int p = 0; p < 4; ++p) kk[h][p] = kbuf[base + p * 64 + lane];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vv[h][i] = vbuf[buf][base + (4 * g + i) * 16 + c];
+        for (int i = 0; i < 4; ++i) vv[h][i] = vbuf[base + (4 * g + i) * 16 + c];
       }
       // Scores of every (tile, block) with p outermost: 4 * NT independent MFMA chains
       // of 4 each (hi and lo parts of q), so the MFMA latency is hidden by the others.
@@ -200,8 +226,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
             x[h * 4 + i] = ok ? v : -INFINITY;
             bmax = fmaxf(bmax, x[h * 4 + i]);
           }
-        bmax = fmaxf(bmax, xor16(bmax));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        bmax = max_xor32(max_xor16(bmax));
         const float mn = fmaxf(m[t], bmax);
         const bool live = mn != -INFINITY;
         float pr[8], rs = 0.0f;
@@ -210,8 +235,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
           pr[i] = live ? __builtin_amdgcn_exp2f(x[i] - mn) : 0.0f;
           rs += pr[i];
         }
-        rs += xor16(rs);
-        rs += __shfl_xor(rs, 32);
+        rs = sum_xor32(sum_xor16(rs));
         // Rescale only when some column's maximum moved (wave-uniform test).
         if (__builtin_amdgcn_ballot_w64(mn != m[t])) {
           const float corr = live ? __builtin_amdgcn_exp2f(m[t] - mn) : 1.0f;
@@ -247,9 +271,22 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
         for (int j = 0; j < 8; ++j)
           acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[j], pl[t], acc[t][j], 0, 0, 0);
     }
-    // No barrier here: the next stage writes the other buffer, and its own barrier is
-    // reached only once every wave has finished this stage.
+  };
+
+  uint32_t slot = 0;
+  for (uint32_t st = 0; st < nst; ++st) {
+    // This wave's loads of stage st are done when at most the kRing - 2 later stages'
+    // (4 loads each) are in flight; the barrier then makes every wave's part visible,
+    // and every wave has finished the stage before (whose slot is refilled next).
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (kRing - 2)) : "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    issue(st + kRing - 1, slot == 0 ? kRing - 1 : slot - 1);
+    compute(&ring[slot][0], &ring[slot][SB * 256], it.blk0 + st * SB);
+    slot = slot + 1 == kRing ? 0 : slot + 1;
   }
+  // No load into LDS may land after the workgroup ends.
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const size_t qd = static_cast<size_t>(hq) * kD;
 #pragma unroll
