@@ -39,7 +39,9 @@ static constexpr int kPrefillTiles = 2;  // MFMA tiles (16 logical rows) per wav
 static constexpr int kPrefillRows = kPrefillWaves * kPrefillTiles * 16;  // logical rows per item
 
 static constexpr int kStageBlocks = 2;  // 16-key blocks per LDS stage (32 keys, 16 KiB of K+V)
-static constexpr int kRing = 6;         // LDS stages: kRing - 1 in flight while one is computed
+static constexpr int kRing = 6;
+static constexpr bool kPrefillSplitP = true;  // P as f16 hi + lo (else one f16 rounding)
+static constexpr float kLazyRescale = 8.0f;    // log2 headroom before the maximum moves         // LDS stages: kRing - 1 in flight while one is computed
 
 // One 16-byte piece per lane from global memory straight into LDS (no registers): lane
 // i's piece lands at LDS byte address `lds` + 16 i. M0 holds the wave's LDS base for
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
       const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float v = has[t] ? x[e] : 0.0f;
+        const float v = has[t] ? x[e] * scale_log2 : 0.0f;  // scores come out in log2 units
         qh[t][pp][e] = static_cast<_Float16>(v);
         ql[t][pp][e] = static_cast<_Float16>(v - static_cast<float>(qh[t][pp][e]));
       }
@@ -215,42 +217,55 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
         // Every key of the pair visible to every row of the tile: no mask needed.
         const bool whole = (key0 + 31 <= tmin[t]) & (key0 >= tlo[t]) & (key0 + 32 <= key_end);
         float x[8], bmax = -INFINITY;
+        if (whole) {  // uniform: the common case needs no mask
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+          for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int kp = key0 + h * 16 + 4 * g + i;
-            const float v = sc[t][h][i] * scale_log2;
-            // Bitwise, not short-circuit: straight-line selects instead of branches.
-            const bool ok = whole | ((kp >= rlo[t]) & (kp <= rpos[t]) & (kp < key_end));
-            x[h * 4 + i] = ok ? v : -INFINITY;
-            bmax = fmaxf(bmax, x[h * 4 + i]);
-          }
-        bmax = max_xor32(max_xor16(bmax));
-        const float mn = fmaxf(m[t], bmax);
-        const bool live = mn != -INFINITY;
-        float pr[8], rs = 0.0f;
+            for (int i = 0; i < 4; ++i) {
+              x[h * 4 + i] = sc[t][h][i];
+              bmax = fmaxf(bmax, x[h * 4 + i]);
+            }
+        } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          pr[i] = live ? __builtin_amdgcn_exp2f(x[i] - mn) : 0.0f;
-          rs += pr[i];
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int kp = key0 + h * 16 + 4 * g + i;
+              // Bitwise, not short-circuit: straight-line selects instead of branches.
+              const bool ok = (kp >= rlo[t]) & (kp <= rpos[t]) & (kp < key_end);
+              x[h * 4 + i] = ok ? sc[t][h][i] : -INFINITY;
+              bmax = fmaxf(bmax, x[h * 4 + i]);
+            }
         }
-        rs = sum_xor32(sum_xor16(rs));
-        // Rescale only when some column's maximum moved (wave-uniform test).
-        if (__builtin_amdgcn_ballot_w64(mn != m[t])) {
-          const float corr = live ? __builtin_amdgcn_exp2f(m[t] - mn) : 1.0f;
+        bmax = max_xor32(max_xor16(bmax));
+        // The running maximum moves only when some column's maximum grew by more than
+        // kLazyRescale (or was still empty): between moves, scores may exceed it by up
+        // to that, so P stays below 2^kLazyRescale, well inside binary16 and f32. The
+        // result is the same softmax (the sum uses the same offset); most stages then
+        // skip the rescale of the accumulators.
+        const float mn = fmaxf(m[t], bmax);
+        if (__builtin_amdgcn_ballot_w64(mn > m[t] + kLazyRescale)) {  // wave-uniform
+          const float corr = mn != -INFINITY ? __builtin_amdgcn_exp2f(m[t] - mn) : 1.0f;
           l[t] *= corr;
 #pragma unroll
           for (int j = 0; j < 8; ++j) acc[t][j] *= corr;
+          m[t] = mn;
         }
+        const bool live = m[t] != -INFINITY;
+        float pr[8], rs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          pr[i] = live ? __builtin_amdgcn_exp2f(x[i] - m[t]) : 0.0f;
+          rs += pr[i];
+        }
+        rs = sum_xor32(sum_xor16(rs));
         l[t] += rs;
-        m[t] = mn;
         // P as an f16 hi part plus an f16 lo part; element e of a lane is key
         // (e / 4) * 16 + 4g + e % 4 of the pair, as the V operand below.
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           ph[t][e] = static_cast<_Float16>(pr[e]);
-          pl[t][e] = static_cast<_Float16>(pr[e] - static_cast<float>(ph[t][e]));
+          if constexpr (kPrefillSplitP) pl[t][e] = static_cast<_Float16>(pr[e] - static_cast<float>(ph[t][e]));
         }
       }
       // PV: every (tile, dim group) hi product, then every lo product, so that the
@@ -265,11 +280,13 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
 #pragma unroll
         for (int j = 0; j < 8; ++j)
           acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[j], ph[t], acc[t][j], 0, 0, 0);
+      if constexpr (kPrefillSplitP) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[j], pl[t], acc[t][j], 0, 0, 0);
+          for (int j = 0; j < 8; ++j)
+            acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[j], pl[t], acc[t][j], 0, 0, 0);
+      }
     }
   };
 
