@@ -6,9 +6,10 @@
  *   Backend::new_kv      (lib.rs:118)  -> yx_kv_create
  *   Backend::copy_page   (lib.rs:120)  -> yx_kv_copy_pages (a batch of PageCopy, kv.rs:35)
  *   Backend::begin_pass  (lib.rs:123)  -> yx_pass_begin    (PassMeta, lib.rs:63-89)
- *   Backend::attention   (lib.rs:132)  -> yx_kv_append (+ yx_attention); the K/V store
- *                                          of write_rows (backend-cpu lib.rs:378-383)
- *                                          and attend (backend-cpu lib.rs:389-427)
+ *   Backend::attention   (lib.rs:132)  -> yx_qk_rope_append_dev (write_rows, backend-cpu
+ *                                          lib.rs:359-385: q/k RMSNorm + RoPE, K/V store)
+ *                                          + yx_attention (attend, lib.rs:389-427); or
+ *                                          yx_kv_append for the K/V store alone
  *
  * Conventions: int status, YX_OK = 0 (codes shared with yaxus_kv_cache.h);
  * yx_last_error() returns a thread-local message; no exception crosses the ABI. Every
@@ -38,7 +39,7 @@ typedef struct yx_kv yx_kv;
 enum { YX_DTYPE_F32 = 0, YX_DTYPE_F16 = 1 };
 enum { YX_K = 0, YX_V = 1 };
 /* Kernels whose launches yx_profile_read reports. */
-enum { YX_KERNEL_ATTENTION = 0, YX_KERNEL_APPEND = 1, YX_KERNEL_COPY = 2 };
+enum { YX_KERNEL_ATTENTION = 0, YX_KERNEL_APPEND = 1, YX_KERNEL_COPY = 2, YX_KERNEL_QK_ROPE = 3 };
 
 const char* yx_last_error(void);
 int yx_device_count(int* n);
@@ -87,6 +88,19 @@ int yx_pass_begin(yx_ctx* ctx, size_t rows, const uint32_t* pos, const uint32_t*
  * to binary16 (nearest-even) and scattered to each row's kv_slot of `layer`. */
 int yx_kv_append(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k, const float* v);
 int yx_kv_append_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k, const float* v);
+
+/* write_rows (backend-cpu lib.rs:359-385; QK_ROPE, yaxus-backend-gpu shaders.rs:285-341),
+ * device pointers: per row of the pass, qkv `[rows][(hq + 2 hkv) * 128]` f32 holds the
+ * q heads, then the k heads, then the v heads. Each q and k head is RMS-normalised
+ * (weights q_norm / k_norm `[128]`, offset 1, eps) and rotated by half-split RoPE at the
+ * row's position; q goes to q_out `[rows][hq * 128]` f32, k and the raw v to the row's
+ * kv_slot of `layer` (binary16, nearest even). rope_cs is the layer's table
+ * `[rope_len][64]` cos then `[rope_len][64]` sin, as Rope::cos_sin (config.rs:213-219)
+ * fills it and the reference GPU backend uploads it (ops/attention.rs:112-120); every
+ * row's position must be below rope_len. The results carry the CPU backend's bits. */
+int yx_qk_rope_append_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* qkv,
+                          const float* q_norm, const float* k_norm, const float* rope_cs,
+                          size_t rope_len, float eps, size_t hq, size_t hkv, float* q_out);
 
 /* attend (backend-cpu lib.rs:389-427; ATTN_SPLIT + ATTN_COMBINE, shaders.rs:1466-1637):
  * causal GQA attention of q `[rows][hq][128]` f32 over each row's keys `[lo, pos]`,

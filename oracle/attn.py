@@ -34,6 +34,7 @@ def lib():
         L.orc_attend.argtypes = [P, S, S, S, S, P, P, P, S, S, P, P, ctypes.c_int, P, ctypes.c_int]
         L.orc_attend_f64.argtypes = [P, S, S, S, S, P, P, P, S, S, P, P, ctypes.c_int, P]
         L.orc_normal.argtypes = [ctypes.c_uint64, ctypes.c_uint64, S, P]
+        L.orc_cos_sin.argtypes = [P, S, ctypes.c_float, S, P, P]
         L.orc_dot.argtypes = [P, P, S]
         L.orc_dot.restype = ctypes.c_float
         _LIB = L
@@ -49,6 +50,15 @@ def normal(n, seed, offset=0):
     host of this image."""
     out = np.empty(int(n), dtype=np.float32)
     lib().orc_normal(seed, offset, int(n), _p(out))
+    return out
+
+
+def cos_sin_table(inv_freq, concentration, n):
+    """`[2][n][half]` cos then sin of positions 0..n-1 (config.rs:213-219)."""
+    f = np.ascontiguousarray(inv_freq, dtype=np.float32)
+    out = np.empty((2, n, f.size), dtype=np.float32)
+    for p in range(n):
+        lib().orc_cos_sin(_p(f), f.size, concentration, p, _p(out[0, p]), _p(out[1, p]))
     return out
 
 

@@ -204,3 +204,46 @@ def test_prefill_tiles_match_oracle(hip, hq, hkv, page, window, chunk):
     err = np.abs(got - want).max()
     assert close(got, want).all(), f"max abs err {err}"
     assert err < 2e-5, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("hq,hkv,page,lens,k", [
+    (16, 4, 16, [1, 300, 17, 64], 1), (8, 8, 16, [5, 40], 33), (32, 2, 128, [200, 1], 3),
+    (16, 1, 16, [0, 1000], 2)])
+def test_qk_rope_append_matches_write_rows(hip, hq, hkv, page, lens, k):
+    """write_rows on the device (RMSNorm + RoPE of q and k, K/V store) gives the CPU
+    backend's bits: q as f32, K and V as their binary16 roundings (orc_write_rows)."""
+    from oracle.attn import cos_sin_table
+    from yaxus_amd.rope import inv_freq, rope_table
+
+    sc = Scenario(hip, pages=200 if page == 16 else 40, page=page, hkv=hkv, pool_seed=6)
+    seqs = [sc.cache.new_seq() for _ in lens]
+    sc.prefill({s: n for s, n in zip(seqs, lens) if n > 0})
+    pr = sc.run_pass([(s, k) for s in seqs])
+    rows = len(pr.meta.pos)
+    qkv = (sc.draw(rows * (hq + 2 * hkv) * D) * 3.0).reshape(rows, -1)
+    qn = sc.draw(D) * 0.1
+    kn = sc.draw(D) * 0.1
+    f = inv_freq(D, 10000.0)
+    conc = 1.2079441
+    table = rope_table(f, conc, 2048)
+    assert np.array_equal(table.view(np.uint32), cos_sin_table(f, conc, 2048).view(np.uint32))
+    q = hip.qk_rope_append(sc.kv, 0, qkv, qn, kn, table, 1e-6, hq)
+    want = sc.orc[0].write_rows(qkv, hq, qn, kn, 1e-6, f, conc, pr.meta.pos, pr.meta.kv_slot)
+    assert np.array_equal(q.view(np.uint32), want.view(np.uint32)), \
+        f"{(q.view(np.uint32) != want.view(np.uint32)).sum()} q values differ, max {np.abs(q - want).max()}"
+    written = sorted(set(int(s) // page for s in pr.meta.kv_slot))
+    _check_pages(sc, 0, written)
+
+
+def test_qk_rope_append_rejects_positions_past_the_table(hip):
+    from yaxus_amd._lib import YxError
+    from yaxus_amd.rope import inv_freq, rope_table
+
+    sc = Scenario(hip, pages=40, page=16, hkv=2)
+    s = sc.cache.new_seq()
+    sc.prefill({s: 100})
+    sc.run_pass([(s, 1)])
+    qkv = np.zeros((1, (8 + 4) * D), np.float32)
+    with pytest.raises(YxError, match="RoPE table"):
+        hip.qk_rope_append(sc.kv, 0, qkv, np.zeros(D), np.zeros(D),
+                           rope_table(inv_freq(D, 10000.0), 1.0, 64), 1e-6, 8)

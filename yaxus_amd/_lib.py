@@ -26,6 +26,7 @@ YX_V = 1
 YX_KERNEL_ATTENTION = 0
 YX_KERNEL_APPEND = 1
 YX_KERNEL_COPY = 2
+YX_KERNEL_QK_ROPE = 3
 
 P = ctypes.c_void_p
 S = ctypes.c_size_t
@@ -81,6 +82,7 @@ HIP_SYMBOLS = {
     "yx_pass_begin": (I, [P, S, P, P, P, P, S]),
     "yx_kv_append": (I, [P, P, S, P, P]),
     "yx_kv_append_dev": (I, [P, P, S, P, P]),
+    "yx_qk_rope_append_dev": (I, [P, P, S, P, P, P, P, S, F, S, S, P]),
     "yx_attention": (I, [P, P, S, P, P, S, S, S, F]),
     "yx_attention_dev": (I, [P, P, S, P, P, S, S, S, F]),
     "yx_attention_append": (I, [P, P, S, P, P, P, P, S, S, S, F]),

@@ -159,6 +159,35 @@ class HipBackend:
             raise ValueError("k/v must be [rows][hkv][head_dim] f32")
         check_hip(self.L.yx_kv_append(self.ctx, kv.h, layer, ptr(k), ptr(v)))
 
+    # write_rows (backend-cpu lib.rs:359-385): q/k RMSNorm + RoPE of the pass's rows, K/V
+    # stored at their slots; returns q. qkv `[rows][(hq + 2 hkv) * d]`, q_norm/k_norm
+    # `[d]`, rope_cs from `rope.rope_table`. DeviceTensors stay on the device; numpy
+    # arrays go through temporaries and q comes back as numpy.
+    def qk_rope_append(self, kv, layer, qkv, q_norm, k_norm, rope_cs, eps, hq, out=None):
+        rope_len = int(rope_cs.shape[1]) if len(rope_cs.shape) == 3 else int(rope_cs.shape[0]) // 2
+        if isinstance(qkv, DeviceTensor):
+            out = out if out is not None else self.tensor((self.rows, hq * kv.d))
+            check_hip(self.L.yx_qk_rope_append_dev(self.ctx, kv.h, layer, qkv.ptr, q_norm.ptr,
+                                                   k_norm.ptr, rope_cs.ptr, rope_len, float(eps),
+                                                   hq, kv.hkv, out.ptr))
+            return out
+        qkv = np.ascontiguousarray(qkv, np.float32)
+        if qkv.size != self.rows * (hq + 2 * kv.hkv) * kv.d:
+            raise ValueError("qkv must be [rows][(hq + 2 hkv) * head_dim] f32")
+        tmp = [self.tensor(a.shape) for a in (qkv, q_norm, k_norm, rope_cs)]
+        try:
+            for t, a in zip(tmp, (qkv, q_norm, k_norm, rope_cs)):
+                t.upload(np.ascontiguousarray(a, np.float32))
+            o = self.tensor((self.rows, hq * kv.d))
+            try:
+                self.qk_rope_append(kv, layer, tmp[0], tmp[1], tmp[2], tmp[3], eps, hq, out=o)
+                return o.numpy()
+            finally:
+                o.free()
+        finally:
+            for t in tmp:
+                t.free()
+
     # The attend half of Backend::attention (backend-cpu lib.rs:389-427)
     def attend(self, kv, layer, q, hq, window=None, scale=None, out=None):
         scale = float(np.float32(1.0) / np.sqrt(np.float32(kv.d))) if scale is None else scale

@@ -47,19 +47,6 @@ __global__ __launch_bounds__(256) void kv_append_f16(const float* __restrict__ k
   *reinterpret_cast<h8*>(dst) = o;
 }
 
-// Backend::copy_page for a hazard-free batch of copies: blockIdx.x = copy, blockIdx.y =
-// (layer, K/V). `bases` holds the 2 * layers arena base pointers (K of layer 0, V of
-// layer 0, K of layer 1, ...). 16-byte loads and stores.
-__global__ __launch_bounds__(256) void kv_copy_pages(const uint32_t* __restrict__ src,
-                                                     const uint32_t* __restrict__ dst,
-                                                     uint4* const* __restrict__ bases,
-                                                     uint32_t page_vec16) {
-  uint4* base = bases[blockIdx.y];
-  const uint4* s = base + static_cast<size_t>(src[blockIdx.x]) * page_vec16;
-  uint4* d = base + static_cast<size_t>(dst[blockIdx.x]) * page_vec16;
-  for (uint32_t i = threadIdx.x; i < page_vec16; i += blockDim.x) d[i] = s[i];
-}
-
 // Plain streaming copy (also the calibration kernel for HBM byte counters).
 __global__ __launch_bounds__(256) void dev_copy16(uint4* __restrict__ d,
                                                   const uint4* __restrict__ s, size_t n) {

@@ -15,6 +15,7 @@
 #include "attn_decode.hpp"
 #include "attn_prefill.hpp"
 #include "kv_kernels.hpp"
+#include "qk_rope.hpp"
 
 namespace {
 
@@ -172,7 +173,7 @@ struct yx_ctx {
   long max_tiles = 4;
   long decode_shape = 0;  // 0: balanced one-tile kernel where it applies, 1: static split only
   bool profiling = false;
-  Profile prof[3];
+  Profile prof[4];
   bool capturing = false;
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
@@ -778,6 +779,36 @@ int yx_kv_append_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const f
   return append_impl(c, kv, layer, k, v);
 }
 
+int yx_qk_rope_append_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* qkv,
+                          const float* q_norm, const float* k_norm, const float* rope_cs,
+                          size_t rope_len, float eps, size_t hq, size_t hkv, float* q_out) {
+  if (!c || !kv || !qkv || !q_norm || !k_norm || !rope_cs || !q_out)
+    return fail(YX_ERR_INVALID, "null argument");
+  int rc = c->set_device();
+  if (rc) return rc;
+  if ((rc = check_kv(c, kv, layer))) return rc;
+  if (hkv != kv->hkv) return fail(YX_ERR_INVALID, "hkv differs from the arena's");
+  if (hq == 0 || hq % hkv != 0) return fail(YX_ERR_INVALID, "hq must be a positive multiple of hkv");
+  if (c->rows == 0) return YX_OK;
+  for (size_t i = 0; i < c->rows; ++i) {
+    if (c->pos[i] >= rope_len) return fail(YX_ERR_INVALID, "a row's position is beyond the RoPE table");
+    if ((c->pos[i] / kv->page) + c->pt_off[i] >= c->npages)
+      return fail(YX_ERR_INVALID, "a row's position has no page-table entry");
+  }
+  if (rope_len > 0xffffffffu) return fail(YX_ERR_UNSUPPORTED, "RoPE table too long");
+  dim3 grid(static_cast<unsigned>(c->rows),
+            static_cast<unsigned>((hq + hkv + yx::kRopeWaves - 1) / yx::kRopeWaves));
+  hipEvent_t e0;
+  if ((rc = prof_begin(c, YX_KERNEL_QK_ROPE, &e0))) return rc;
+  hipLaunchKernelGGL(yx::qk_norm_rope_append, grid, dim3(64 * yx::kRopeWaves), 0, c->stream, qkv,
+                     q_norm, k_norm, rope_cs, static_cast<uint32_t>(rope_len), eps,
+                     static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_slot.p),
+                     kv->k[layer], kv->v[layer], q_out, static_cast<uint32_t>(hq),
+                     static_cast<uint32_t>(hkv), static_cast<uint32_t>(kv->page));
+  YX_HIP(hipGetLastError());
+  return prof_end(c, YX_KERNEL_QK_ROPE, e0);
+}
+
 int yx_kv_append(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v) {
   if (!c || !kv) return fail(YX_ERR_INVALID, "null argument");
   int rc = c->set_device();
@@ -974,7 +1005,7 @@ int yx_profile_enable(yx_ctx* c, int on) {
 }
 
 int yx_profile_read(yx_ctx* c, int kernel, double* total_ms, uint64_t* launches) {
-  if (!c || kernel < 0 || kernel > 2) return fail(YX_ERR_INVALID, "bad context or kernel");
+  if (!c || kernel < 0 || kernel > 3) return fail(YX_ERR_INVALID, "bad context or kernel");
   int rc = c->set_device();
   if (rc) return rc;
   YX_HIP(hipStreamSynchronize(c->stream));
