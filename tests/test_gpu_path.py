@@ -247,3 +247,53 @@ def test_qk_rope_append_rejects_positions_past_the_table(hip):
     with pytest.raises(YxError, match="RoPE table"):
         hip.qk_rope_append(sc.kv, 0, qkv, np.zeros(D), np.zeros(D),
                            rope_table(inv_freq(D, 10000.0), 1.0, 64), 1e-6, 8)
+
+
+@pytest.mark.parametrize("window", [None, 16])
+def test_model_attention_two_passes_across_pages(hip, window):
+    """backend-cpu lib.rs:676-714 at head_dim 128 on the device: two sequences on the
+    non-adjacent pages [3, 1] and [0], lengths 140 and 9, written in two passes that
+    cross a page boundary (PAGE = 128), through Backend::attention in full (write_rows
+    then attend), against the oracle's write_rows + attend on the same f16 arena."""
+    from types import SimpleNamespace
+
+    from oracle.attn import OracleArena
+    from tests.test_attn_oracle import _values
+    from yaxus_amd.rope import rope_table
+
+    hq, hkv, P, eps = 4, 2, 128, 1e-6
+    f = np.array([1.0 / 10000.0 ** (i / 64) for i in range(64)], np.float32)
+    conc = 1.1
+    table = rope_table(f, conc, 256)
+    cols = (hq + 2 * hkv) * D
+    pages = [[3, 1], [0]]
+    lens = [140, 9]
+    qkv = [[_values(cols, s * 1000 + p) for p in range(n)] for s, n in enumerate(lens)]
+    qn = _values(D, 7) * np.float32(0.5)
+    kn = _values(D, 8) * np.float32(0.5)
+    kv = hip.new_kv(1, 4, P, hkv)
+    orc = OracleArena(4, P, hkv, D, f16=True)
+    first = [(0, p) for p in range(100)] + [(1, p) for p in range(4)]
+    second = [(0, p) for p in range(100, 140)] + [(1, p) for p in range(4, 9)]
+    for rows in (first, second):
+        meta_pages, off = [], {}
+        for sq, _ in rows:
+            if sq not in off:
+                off[sq] = len(meta_pages)
+                meta_pages += pages[sq]
+        meta = SimpleNamespace(
+            pos=np.array([p for _, p in rows], np.uint32),
+            kv_slot=np.array([pages[s][p // P] * P + p % P for s, p in rows], np.uint32),
+            pt_off=np.array([off[s] for s, _ in rows], np.uint32),
+            pages=np.array(meta_pages, np.uint32))
+        x = np.stack([qkv[s][p] for s, p in rows])
+        hip.begin_pass(meta)
+        got = hip.attention(kv, 0, x, qn, kn, table, eps, hq, window=window)
+        q = orc.write_rows(x, hq, qn, kn, eps, f, conc, meta.pos, meta.kv_slot)
+        want = orc.attend(q, hq, meta.pos, meta.pt_off, meta.pages, window=window or 0)
+        assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
+    k, v = kv.read_pages(0, [0, 1, 3])
+    for i, p in enumerate([0, 1, 3]):
+        ok, ov = orc.page_bits(p)
+        assert np.array_equal(k[i], ok) and np.array_equal(v[i], ov)
+    kv.destroy()

@@ -188,6 +188,19 @@ class HipBackend:
             for t in tmp:
                 t.free()
 
+    # Backend::attention (lib.rs:132; backend-cpu lib.rs:516-530): write_rows, then attend
+    # the rows' queries. Device tensors stay on the device (no synchronisation).
+    def attention(self, kv, layer, qkv, q_norm, k_norm, rope_cs, eps, hq, window=None,
+                  scale=None, out=None):
+        if isinstance(qkv, DeviceTensor):
+            q = self.qk_rope_append(kv, layer, qkv, q_norm, k_norm, rope_cs, eps, hq)
+            try:
+                return self.attend(kv, layer, q, hq, window=window, scale=scale, out=out)
+            finally:
+                q.free()
+        q = self.qk_rope_append(kv, layer, qkv, q_norm, k_norm, rope_cs, eps, hq)
+        return self.attend(kv, layer, q, hq, window=window, scale=scale)
+
     # The attend half of Backend::attention (backend-cpu lib.rs:389-427)
     def attend(self, kv, layer, q, hq, window=None, scale=None, out=None):
         scale = float(np.float32(1.0) / np.sqrt(np.float32(kv.d))) if scale is None else scale

@@ -5,17 +5,34 @@ that touch the KV cache: ``begin`` / ``start`` / ``prefill`` / ``forward`` / ``f
 / ``fork`` / ``truncate`` and the page copies an operation asks for, which are made
 before the next pass even when the operation fails (kv.rs:4-7, lib.rs:349-353, 441-444).
 The weight products around attention are out of scope: ``forward`` takes, per layer,
-the rows' ``(k, v, q)`` from a caller-supplied function, stores K/V and attends
+the rows' inputs from a caller-supplied function and runs the layer's attention
 through the backend (``HipBackend`` on a GPU; any object with the same methods, such
-as the do-nothing backend of the tests, otherwise).
+as the do-nothing backend of the tests, otherwise). The inputs are either a
+``LayerQkv`` (the projected rows and the layer's norm weights and RoPE table:
+``Backend::attention`` in full, write_rows then attend) or ``(k, v, q)`` already
+normalised and rotated (the K/V store and attend only).
 """
 
 from __future__ import annotations
+
+from typing import NamedTuple
 
 from .kv import KvCache, KvError
 
 DEFAULT_KV_TOKENS = 16384  # lib.rs:238
 DEFAULT_MAX_POS = 8192  # lib.rs:239
+
+
+class LayerQkv(NamedTuple):
+    """One layer's attention inputs as ``Backend::attention`` takes them (lib.rs:132):
+    qkv ``[rows][(hq + 2 hkv) * d]``, q_norm/k_norm ``[d]``, the RoPE table of the
+    layer's kind (``rope.rope_table``) and the RMSNorm eps."""
+
+    qkv: object
+    q_norm: object
+    k_norm: object
+    rope_cs: object
+    eps: float
 
 
 class ModelError(Exception):
@@ -115,7 +132,13 @@ class PagedModel:
             if layer_inputs is None:
                 outs.append(None)
                 continue
-            k, v, q = layer_inputs(layer, pr.meta)
+            inp = layer_inputs(layer, pr.meta)
+            if isinstance(inp, LayerQkv):
+                outs.append(self.backend.attention(self.kv, layer, inp.qkv, inp.q_norm,
+                                                   inp.k_norm, inp.rope_cs, inp.eps, self.hq,
+                                                   window=self.windows[layer]))
+                continue
+            k, v, q = inp
             outs.append(self.backend.attend_append(self.kv, layer, k, v, q, self.hq,
                                                    window=self.windows[layer]))
         return pr, outs
@@ -130,4 +153,4 @@ class PagedModel:
         return out
 
 
-__all__ = ["PagedModel", "ModelError", "KvError", "DEFAULT_KV_TOKENS", "DEFAULT_MAX_POS"]
+__all__ = ["PagedModel", "LayerQkv", "ModelError", "KvError", "DEFAULT_KV_TOKENS", "DEFAULT_MAX_POS"]
