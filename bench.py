@@ -150,6 +150,35 @@ def _time_layers(hip, kv, pr, layers, hq, windows, steps, extra=None):
     return us
 
 
+def _time_write_rows(hip, kv, pr, layers, steps):
+    """write_rows (q/k RMSNorm + RoPE + K/V store) per layer for the pass `pr`:
+    (us per layer, bytes per layer: qkv read, q written, K/V written)."""
+    from yaxus_amd.rope import inv_freq, rope_table
+
+    rows = len(pr.meta.pos)
+    cols = (HQ + 2 * HKV) * D
+    qkv = hip.tensor((rows, cols))
+    hip.fill_normal(qkv.ptr, rows * cols, False, SEED + 77, 0)
+    qn, kn = hip.tensor((D,)), hip.tensor((D,))
+    hip.fill_normal(qn.ptr, D, False, SEED + 78, 0)
+    hip.fill_normal(kn.ptr, D, False, SEED + 79, 0)
+    table = rope_table(inv_freq(D, 10000.0), 1.0, int(max(pr.meta.pos)) + 1)
+    cs = hip.tensor(table.shape).upload(table)
+    q = hip.tensor((rows, HQ * D))
+    hip.begin_pass(pr.meta)
+    for l in range(layers):
+        hip.qk_rope_append(kv, l, qkv, qn, kn, cs, 1e-6, HQ, out=q)
+    hip.sync()
+    hip.timer_start()
+    for _ in range(steps):
+        for l in range(layers):
+            hip.qk_rope_append(kv, l, qkv, qn, kn, cs, 1e-6, HQ, out=q)
+    us = hip.timer_stop() * 1000.0 / (steps * layers)
+    for t in (qkv, qn, kn, cs, q):
+        t.free()
+    return us, rows * (cols * 4 + HQ * D * 4 + HKV * D * 2 * 2)
+
+
 def bench_configs(hip, steps=10, include_long=True):
     """BASELINE configurations 2-5 at full size (one JSON object per configuration)."""
     from yaxus_amd import KvCache
@@ -174,10 +203,12 @@ def bench_configs(hip, steps=10, include_long=True):
     ctx = [1024 + int(n) + 1 for n in suf]
     logical = sum(ctx) * HKV * D * 2 * 2
     unique = (1024 + int(sum(suf)) + B) * HKV * D * 2 * 2
+    wr_us, wr_bytes = _time_write_rows(hip, kv, pr, layers, steps)
     res["cfg2_prefix_decode"] = {"us_per_layer_step": round(us, 2),
                                  "logical_GBs": round(logical / us / 1e3, 1),
                                  "unique_GBs": round(unique / us / 1e3, 1),
-                                 "logical_bytes": logical, "unique_bytes": unique}
+                                 "logical_bytes": logical, "unique_bytes": unique,
+                                 "write_rows_us_per_layer": round(wr_us, 2)}
     kv.destroy()
     # cfg3: 16 requests append a 256-token chunk on contexts U[0, 2048] that leave a
     # half-filled tail page; causal within the chunk; 24 layers.
@@ -193,10 +224,13 @@ def bench_configs(hip, steps=10, include_long=True):
     _fill_arena(hip, kv, layers, SEED + 3)
     us = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, max(2, steps // 2)) / layers
     flops = sum(4 * HQ * D * (256 * p + 256 * 257 // 2) for p in prior)
+    wr_us, wr_bytes = _time_write_rows(hip, kv, pr, layers, max(2, steps // 2))
     res["cfg3_chunked_prefill"] = {"us_per_layer_step": round(us, 2),
                                    "TFLOPs": round(flops / us / 1e6, 2),
                                    "mfma_util_vs_2.5PF": round(flops / us / 1e6 / 2500.0, 4),
-                                   "flops_per_layer": flops}
+                                   "flops_per_layer": flops,
+                                   "write_rows_us_per_layer": round(wr_us, 2),
+                                   "write_rows_GBs": round(wr_bytes / wr_us / 1e3, 1)}
     kv.destroy()
     # cfg5: 16 requests of ctx 4096 (2048 shared) verify 5 draft tokens (5 causal
     # rows each); then 8 fork from a partly filled tail page (copy on write) and roll
