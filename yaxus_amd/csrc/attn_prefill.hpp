@@ -34,8 +34,8 @@ struct PrefillItem {
   uint32_t pad[3];
 };
 
-static constexpr int kPrefillWaves = 4;
-static constexpr int kPrefillTiles = 2;  // MFMA tiles (16 logical rows) per wave
+static constexpr int kPrefillWaves = 8;
+static constexpr int kPrefillTiles = 1;  // MFMA tiles (16 logical rows) per wave
 static constexpr int kPrefillRows = kPrefillWaves * kPrefillTiles * 16;  // logical rows per item
 
 static constexpr int kStageBlocks = 2;  // 16-key blocks per LDS stage (32 keys, 16 KiB of K+V)
@@ -59,7 +59,9 @@ __device__ __forceinline__ void load_to_lds16(const void* src, uint32_t lds) {
       : "memory");
 }
 
-__global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
+// Two waves per SIMD (at most 256 registers each), so one wave's softmax arithmetic
+// overlaps the other's matrix products.
+__global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_attn_prefill(
     const PrefillItem* __restrict__ items, const uint32_t* pos,
     const uint32_t* __restrict__ pages, const _Float16* __restrict__ kc,
     const _Float16* __restrict__ vc, const float* q, float* __restrict__ out,
@@ -79,11 +81,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
   const uint32_t bpp_mask = (1u << bpp_shift) - 1u;
   const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;
   const uint32_t* pt = pages + it.pt_off;
-  // Each wave moves a quarter of a stage: wave w takes block w / 2 of the stage, its K
-  // (w even) or V (w odd), as four 1 KiB rows. K row p is read transposed ([p][key][g]
-  // in the arena, [p][g][key] in LDS): lane l fetches key l % 16, dims group l / 16.
-  const uint32_t my_blk = static_cast<uint32_t>(wave >> 1);
-  const bool my_v = (wave & 1) != 0;
+  // Each wave moves an eighth of a stage: wave w takes block w / 4 of the stage, its K
+  // ((w / 2) even) or V, as the two 1 KiB rows 2 (w % 2) and 2 (w % 2) + 1. K row p is read
+  // transposed ([p][key][g] in the arena, [p][g][key] in LDS): lane l fetches key l % 16,
+  // dims group l / 16.
+  static_assert(kPrefillWaves == 8 && SB == 2, "the stage split below assumes 8 waves, 2 blocks");
+  constexpr int kRowsPerWave = 2;  // 1 KiB rows (loads) per wave per stage
+  const uint32_t my_blk = static_cast<uint32_t>(wave >> 2);
+  const bool my_v = ((wave >> 1) & 1) != 0;
+  const uint32_t my_row0 = static_cast<uint32_t>(wave & 1) * kRowsPerWave;
   const uint32_t lane_src = my_v ? static_cast<uint32_t>(lane) * 16u
                                  : static_cast<uint32_t>((lane & 15) * 4 + (lane >> 4)) * 16u;
   const char* my_arena = reinterpret_cast<const char*>(my_v ? vc : kc);
@@ -98,7 +104,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
     const uint32_t dst = ring_base + slot * (2 * SB * 256 * 16) +
                          (my_v ? SB * 4096u : 0u) + my_blk * 4096u;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) load_to_lds16(blk + r * 1024 + lane_src, dst + r * 1024);
+    for (int r = 0; r < kRowsPerWave; ++r)
+      load_to_lds16(blk + (my_row0 + r) * 1024 + lane_src, dst + (my_row0 + r) * 1024);
   };
   // q and pos are read first, unconditionally (rows past the tile read row 0 and are
   // zeroed), so that waiting for them does not wait for the K/V stages issued after.
@@ -190,27 +197,24 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
 #pragma unroll
         for (int i = 0; i < 4; ++i) vv[h][i] = vbuf[base + (4 * g + i) * 16 + c];
       }
-      // Scores of every (tile, block) with p outermost: 4 * NT independent MFMA chains
-      // of 4 each (hi and lo parts of q), so the MFMA latency is hidden by the others.
-      floatx4 sh[NT][2], sl[NT][2];
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) sh[t][h] = sl[t][h] = floatx4{0, 0, 0, 0};
-#pragma unroll
-      for (int p = 0; p < 4; ++p)
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            sh[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk[h][p], qh[t][p], sh[t][h], 0, 0, 0);
-            sl[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk[h][p], ql[t][p], sl[t][h], 0, 0, 0);
-          }
+      // Scores of every (tile, block): 2 * NT accumulators, each taking the hi-part
+      // products for p = 0..3 and then the lo-part ones, so consecutive products into one
+      // accumulator are 2 * NT MFMAs apart and no add joins the parts afterwards.
       floatx4 sc[NT][2];
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) sc[t][h] = sh[t][h] + sl[t][h];
+        for (int h = 0; h < 2; ++h) sc[t][h] = floatx4{0, 0, 0, 0};
+#pragma unroll
+      for (int part = 0; part < 2; ++part)
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+              sc[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk[h][p], part ? ql[t][p] : qh[t][p],
+                                                                sc[t][h], 0, 0, 0);
       half8 ph[NT], pl[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -251,7 +255,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
           for (int j = 0; j < 8; ++j) acc[t][j] *= corr;
           m[t] = mn;
         }
-        const bool live = m[t] != -INFINITY;
+        // A whole tile has a finite maximum by now; otherwise a column that has seen no
+        // key yet (maximum -inf) gets zeros.
+        const bool live = whole || m[t] != -INFINITY;
         float pr[8], rs = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -293,9 +299,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void paged_attn_prefill(
   uint32_t slot = 0;
   for (uint32_t st = 0; st < nst; ++st) {
     // This wave's loads of stage st are done when at most the kRing - 2 later stages'
-    // (4 loads each) are in flight; the barrier then makes every wave's part visible,
+    // (kRowsPerWave loads each) are in flight; the barrier then makes every wave's part visible,
     // and every wave has finished the stage before (whose slot is refilled next).
-    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (kRing - 2)) : "memory");
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(kRowsPerWave * (kRing - 2)) : "memory");
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
     issue(st + kRing - 1, slot == 0 ? kRing - 1 : slot - 1);
