@@ -38,10 +38,10 @@ static constexpr int kPrefillWaves = 8;
 static constexpr int kPrefillTiles = 1;  // MFMA tiles (16 logical rows) per wave
 static constexpr int kPrefillRows = kPrefillWaves * kPrefillTiles * 16;  // logical rows per item
 
-static constexpr int kStageBlocks = 2;  // 16-key blocks per LDS stage (32 keys, 16 KiB of K+V)
-static constexpr int kRing = 6;
+static constexpr int kStageBlocks = 4;  // 16-key blocks per LDS stage (64 keys, 32 KiB of K+V)
+static constexpr int kRing = 4;         // LDS stages: kRing - 1 in flight while one is computed
 static constexpr bool kPrefillSplitP = true;  // P as f16 hi + lo (else one f16 rounding)
-static constexpr float kLazyRescale = 8.0f;    // log2 headroom before the maximum moves         // LDS stages: kRing - 1 in flight while one is computed
+static constexpr float kLazyRescale = 8.0f;    // log2 headroom before the maximum moves
 
 // One 16-byte piece per lane from global memory straight into LDS (no registers): lane
 // i's piece lands at LDS byte address `lds` + 16 i. M0 holds the wave's LDS base for
@@ -81,15 +81,14 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
   const uint32_t bpp_mask = (1u << bpp_shift) - 1u;
   const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;
   const uint32_t* pt = pages + it.pt_off;
-  // Each wave moves an eighth of a stage: wave w takes block w / 4 of the stage, its K
-  // ((w / 2) even) or V, as the two 1 KiB rows 2 (w % 2) and 2 (w % 2) + 1. K row p is read
-  // transposed ([p][key][g] in the arena, [p][g][key] in LDS): lane l fetches key l % 16,
-  // dims group l / 16.
-  static_assert(kPrefillWaves == 8 && SB == 2, "the stage split below assumes 8 waves, 2 blocks");
-  constexpr int kRowsPerWave = 2;  // 1 KiB rows (loads) per wave per stage
-  const uint32_t my_blk = static_cast<uint32_t>(wave >> 2);
-  const bool my_v = ((wave >> 1) & 1) != 0;
-  const uint32_t my_row0 = static_cast<uint32_t>(wave & 1) * kRowsPerWave;
+  // Each wave moves an eighth of a stage: wave w takes block w / 2 of the stage, its K
+  // (w even) or V (w odd), as four 1 KiB rows. K row p is read transposed ([p][key][g] in
+  // the arena, [p][g][key] in LDS): lane l fetches key l % 16, dims group l / 16.
+  static_assert(kPrefillWaves == 8 && SB == 4, "the stage split below assumes 8 waves, 4 blocks");
+  constexpr int kRowsPerWave = 4;  // 1 KiB rows (loads) per wave per stage
+  const uint32_t my_blk = static_cast<uint32_t>(wave >> 1);
+  const bool my_v = (wave & 1) != 0;
+  const uint32_t my_row0 = 0;
   const uint32_t lane_src = my_v ? static_cast<uint32_t>(lane) * 16u
                                  : static_cast<uint32_t>((lane & 15) * 4 + (lane >> 4)) * 16u;
   const char* my_arena = reinterpret_cast<const char*>(my_v ? vc : kc);
