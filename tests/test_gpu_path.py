@@ -81,11 +81,11 @@ def option(hip, key, value):
 # attn_decode_shape: 0 = the balanced one-tile kernel where it applies (waves share a
 # queue of quads), 1 = the static-split kernel only.
 @pytest.mark.parametrize("shape", [0, 1])
-@pytest.mark.parametrize("page", [16, 128])
+@pytest.mark.parametrize("page", [16, 32, 64, 128])
 @pytest.mark.parametrize("window", [0, 100])
 def test_decode_matches_oracle(hip, page, window, shape):
     hq, hkv = 16, 4
-    sc = Scenario(hip, pages=256 if page == 16 else 48, page=page, hkv=hkv, pool_seed=11)
+    sc = Scenario(hip, pages=256 * 16 // page + 16, page=page, hkv=hkv, pool_seed=11)
     lens = [1, 15, 16, 17, 300, 1000, 33, 250]
     seqs = [sc.cache.new_seq() for _ in lens]
     sc.prefill(dict(zip(seqs, lens)))
@@ -185,11 +185,11 @@ def test_attention_is_deterministic(hip, shape):
 
 @pytest.mark.parametrize("hq,hkv,page,window,chunk", [
     (16, 4, 16, 0, 256), (16, 4, 16, 100, 64), (8, 8, 16, 0, 40), (32, 2, 128, 0, 96),
-    (16, 4, 128, 300, 33)])
+    (16, 4, 128, 300, 33), (16, 4, 32, 0, 70), (8, 2, 64, 50, 129)])
 def test_prefill_tiles_match_oracle(hip, hq, hkv, page, window, chunk):
     """Chunked prefill (many rows per sequence): the MFMA tile kernel over LDS-staged
     K/V, causal within the chunk and full (or windowed) over the earlier context."""
-    sc = Scenario(hip, pages=420 if page == 16 else 60, page=page, hkv=hkv, pool_seed=12)
+    sc = Scenario(hip, pages=420 * 16 // page + 12, page=page, hkv=hkv, pool_seed=12)
     prior = [8, 0, 1000, 517]
     seqs = [sc.cache.new_seq() for _ in prior]
     sc.prefill({s: n for s, n in zip(seqs, prior) if n})
