@@ -21,9 +21,8 @@
 //   K: A operand of QK, lane holds key c, dims p*32 + g*8 + 0..7 for MFMA p. The arena
 //      stores each 16-key block of K as [p][key][32 dims] (see kv_kernels.hpp), so the
 //      64 lanes' 16-byte loads of one MFMA read 1 KiB contiguous.
-//   V: A operand of PV, lane holds dim c*8 + j of keys 4g..4g+3 for MFMA j. The arena
-//      stores each 16-key block of V in that order (v_offset, kv_kernels.hpp): load jp
-//      gives a lane the operands of MFMAs 2jp and 2jp+1, 1 KiB contiguous per load.
+//   V: A operand of PV, lane holds dims c*8 + j of keys 4g..4g+3; V rows are stored
+//      plainly ([key][128 dims]), so each of the 4 loads reads 4 rows contiguous.
 //   The PV output lands as 32 consecutive dims (32g..32g+31) of column c per lane.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -131,9 +130,9 @@ __device__ __forceinline__ void load_block(BlockRegs& r, const _Float16* __restr
   const half8* kp = reinterpret_cast<const half8*>(kblk) + c * 4 + g;  // [p][key c][g]
 #pragma unroll
   for (int p = 0; p < 4; ++p) r.k[p] = __builtin_nontemporal_load(kp + p * 64);
-  const half8* vp = reinterpret_cast<const half8*>(vblk) + lane;  // [jp][lane] (v_offset)
+  const half8* vp = reinterpret_cast<const half8*>(vblk + (4 * g) * kD + c * 8);
 #pragma unroll
-  for (int jp = 0; jp < 4; ++jp) r.v[jp] = __builtin_nontemporal_load(vp + jp * 64);
+  for (int i = 0; i < 4; ++i) r.v[i] = __builtin_nontemporal_load(vp + i * (kD / 8));
 }
 
 // Waves per workgroup (W): they share one work item's blocks and merge through LDS.
@@ -170,17 +169,13 @@ __device__ __forceinline__ void fused_append(const AttnItem& it, uint32_t kh, ui
     const uint32_t slot = kv_slot[row];
     const uint32_t off = slot & (page_size - 1);
     const size_t region = (static_cast<size_t>(slot >> (bpp_shift + 4)) * hkv + kh) * page_size * kD;
+    _Float16* dst = is_k ? kw + region + k_offset(off, ch) : vw + region + off * kD + ch * 8;
     const float4 a = *reinterpret_cast<const float4*>(src);
     const float4 b = *reinterpret_cast<const float4*>(src + 4);
-    const half8 o = {static_cast<_Float16>(a.x), static_cast<_Float16>(a.y), static_cast<_Float16>(a.z),
-                     static_cast<_Float16>(a.w), static_cast<_Float16>(b.x), static_cast<_Float16>(b.y),
-                     static_cast<_Float16>(b.z), static_cast<_Float16>(b.w)};
-    if (is_k) {
-      *reinterpret_cast<half8*>(kw + region + k_offset(off, ch)) = o;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vw[region + v_offset(off, ch * 8 + e)] = o[e];
-    }
+    *reinterpret_cast<half8*>(dst) =
+        half8{static_cast<_Float16>(a.x), static_cast<_Float16>(a.y), static_cast<_Float16>(a.z),
+              static_cast<_Float16>(a.w), static_cast<_Float16>(b.x), static_cast<_Float16>(b.y),
+              static_cast<_Float16>(b.z), static_cast<_Float16>(b.w)};
   }
   // Stores complete, then the workgroup barrier orders them before every wave's loads
   // (the waves of a workgroup share one CU and its L1).
@@ -423,9 +418,8 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int jp = j / 2, e0 = (j & 1) * 4;  // keys 4g..4g+3 of dim c*8+j (v_offset)
-        const half8 a = {r[0].v[jp][e0], r[0].v[jp][e0 + 1], r[0].v[jp][e0 + 2], r[0].v[jp][e0 + 3],
-                         r[1].v[jp][e0], r[1].v[jp][e0 + 1], r[1].v[jp][e0 + 2], r[1].v[jp][e0 + 3]};
+        const half8 a = {r[0].v[0][j], r[0].v[1][j], r[0].v[2][j], r[0].v[3][j],
+                         r[1].v[0][j], r[1].v[1][j], r[1].v[2][j], r[1].v[3][j]};
         acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, acc[t][j], 0, 0, 0);
       }
     }
@@ -533,8 +527,8 @@ __device__ __forceinline__ void load_block_buf(BlockRegs& r, const _Float16* kbl
   for (int p = 0; p < 4; ++p)  // [p][key c][g] in 16-byte units
     r.k[p] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, ((c * 4 + g) + p * 64) * 16, 0, kNontemporal));
 #pragma unroll
-  for (int jp = 0; jp < 4; ++jp)  // dims c*8+2jp, +1 of keys 4g..4g+3 (v_offset)
-    r.v[jp] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, (jp * 64 + lane) * 16, 0, kNontemporal));
+  for (int i = 0; i < 4; ++i)  // key 4g + i, dims c*8..c*8+7
+    r.v[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, ((4 * g + i) * kD + c * 8) * 2, 0, kNontemporal));
 }
 
 __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
@@ -669,8 +663,7 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int jp = j / 2, e0 = (j & 1) * 4;  // keys 4g..4g+3 of dim c*8+j (v_offset)
-      const half4 a = {r.v[jp][e0], r.v[jp][e0 + 1], r.v[jp][e0 + 2], r.v[jp][e0 + 3]};
+      const half4 a = {r.v[0][j], r.v[1][j], r.v[2][j], r.v[3][j]};
       acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb, acc[j], 0, 0, 0);
     }
   };

@@ -194,7 +194,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
 #pragma unroll
         for (int p = 0; p < 4; ++p) kk[h][p] = kbuf[base + p * 64 + lane];
 #pragma unroll
-        for (int jp = 0; jp < 4; ++jp) vv[h][jp] = vbuf[base + jp * 64 + lane];  // v_offset order
+        for (int i = 0; i < 4; ++i) vv[h][i] = vbuf[base + (4 * g + i) * 16 + c];
       }
       // Scores of every (tile, block): 2 * NT accumulators, each taking the hi-part
       // products for p = 0..3 and then the lo-part ones, so consecutive products into one
@@ -278,10 +278,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
       half8 va[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        va[j] = half8{vv[0][j / 2][(j & 1) * 4], vv[0][j / 2][(j & 1) * 4 + 1],
-                      vv[0][j / 2][(j & 1) * 4 + 2], vv[0][j / 2][(j & 1) * 4 + 3],
-                      vv[1][j / 2][(j & 1) * 4], vv[1][j / 2][(j & 1) * 4 + 1],
-                      vv[1][j / 2][(j & 1) * 4 + 2], vv[1][j / 2][(j & 1) * 4 + 3]};
+        va[j] = half8{vv[0][0][j], vv[0][1][j], vv[0][2][j], vv[0][3][j],
+                      vv[1][0][j], vv[1][1][j], vv[1][2][j], vv[1][3][j]};
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll

@@ -1,13 +1,10 @@
-// K/V store and data-fill kernels for the paged arena.
+// K/V store, page copy and data-fill kernels for the paged arena.
 //
-// Arena layout per layer, binary16: a (page, kv head) is one contiguous region of
-// page_size x 128 halves for K and one for V, made of 16-key blocks of 2048 halves
-// (4 KiB). Within a block the order is the one in which the attention kernels' MFMA
-// operand loads read it, so each load instruction of a wave reads 1 KiB contiguous:
-//   K: dim d of key k at (d / 32) * 512 + k * 32 + d % 32        (k_offset)
-//   V: dim d of key k at ((d % 8) / 2) * 512 + (d / 8 + 16 (k / 4)) * 8 + (d % 2) * 4 + k % 4
-//      (v_offset): lane L = d / 8 + 16 (k / 4) of load jp = (d % 8) / 2 holds the four
-//      keys 4 (k / 4) .. +3 of dims d and d + 1 -- two PV operands of four keys each.
+// Arena layout per layer, binary16: V is `[page][kv_head][page_size][128]`; K is the
+// same but each 16-key block of a (page, kv head) is stored `[4][16 keys][32 dims]`:
+// dim d of key k of the block sits at (d / 32) * 512 + k * 32 + d % 32. That is the
+// order in which the attention kernel's MFMA operand loads read it (1 KiB contiguous
+// per load instruction).
 
 #pragma once
 #include <hip/hip_runtime.h>
@@ -21,18 +18,11 @@ __host__ __device__ inline size_t k_offset(uint32_t off, uint32_t ch) {
   return static_cast<size_t>(off / 16) * 2048 + (ch / 4) * 512 + (off % 16) * 32 + (ch % 4) * 8;
 }
 
-// Offset in halves of (key `off` of a page, dim d) within a (page, kv head) region of V.
-__host__ __device__ inline size_t v_offset(uint32_t off, uint32_t d) {
-  const uint32_t k = off % 16;
-  return static_cast<size_t>(off / 16) * 2048 + ((d % 8) / 2) * 512 + (d / 8 + 16 * (k / 4)) * 8 +
-         (d % 2) * 4 + k % 4;
-}
-
 // The K/V store of write_rows (crates/yaxus-backend-cpu/src/lib.rs:378-383): one
 // thread per 8 consecutive dims of one (row, kv head); two 16-byte f32 loads, a
-// round-to-nearest-even conversion, one 16-byte store for K (16 consecutive threads
-// write one key's four 64-byte pieces), eight 2-byte stores for V (a key's dims are
-// spread over the block's operand order). blockIdx.y: 0 = K, 1 = V.
+// round-to-nearest-even conversion, one 16-byte store. blockIdx.y: 0 = K, 1 = V.
+// 16 consecutive threads write one key's 256 bytes (V: one contiguous row; K: four
+// contiguous 64-byte pieces).
 __global__ __launch_bounds__(256) void kv_append_f16(const float* __restrict__ k,
                                                      const float* __restrict__ v,
                                                      const uint32_t* __restrict__ kv_slot,
@@ -47,19 +37,14 @@ __global__ __launch_bounds__(256) void kv_append_f16(const float* __restrict__ k
   const uint32_t slot = kv_slot[row];
   const uint32_t page = slot / page_size, off = slot % page_size;
   const size_t region = (static_cast<size_t>(page) * hkv + h) * page_size * 128;
+  _Float16* dst = blockIdx.y == 0 ? kc + region + k_offset(off, ch) : vc + region + off * 128 + ch * 8;
   const float4 a = *reinterpret_cast<const float4*>(src);
   const float4 b = *reinterpret_cast<const float4*>(src + 4);
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   h8 o = {static_cast<_Float16>(a.x), static_cast<_Float16>(a.y), static_cast<_Float16>(a.z),
           static_cast<_Float16>(a.w), static_cast<_Float16>(b.x), static_cast<_Float16>(b.y),
           static_cast<_Float16>(b.z), static_cast<_Float16>(b.w)};
-  if (blockIdx.y == 0) {
-    *reinterpret_cast<h8*>(kc + region + k_offset(off, ch)) = o;
-  } else {
-    _Float16* vr = vc + region;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) vr[v_offset(off, ch * 8 + e)] = o[e];
-  }
+  *reinterpret_cast<h8*>(dst) = o;
 }
 
 // Plain streaming copy (also the calibration kernel for HBM byte counters).

@@ -77,8 +77,8 @@ __global__ __launch_bounds__(64 * kRopeWaves) void qk_norm_rope_append(
   kc[region + k_offset(off, lane / 8) + lane % 8] = static_cast<_Float16>(o0);
   kc[region + k_offset(off, (lane + 64) / 8) + lane % 8] = static_cast<_Float16>(o1);
   const float* vsrc = src + kvd;  // the value head follows the key heads
-  vc[region + v_offset(off, lane)] = static_cast<_Float16>(vsrc[lane]);
-  vc[region + v_offset(off, lane + 64)] = static_cast<_Float16>(vsrc[lane + 64]);
+  vc[region + off * 128 + lane] = static_cast<_Float16>(vsrc[lane]);
+  vc[region + off * 128 + lane + 64] = static_cast<_Float16>(vsrc[lane + 64]);
 }
 
 }  // namespace yx

@@ -656,8 +656,8 @@ int yx_kv_copy_pages(yx_ctx* c, yx_kv* kv, const uint32_t* src, const uint32_t* 
   return YX_OK;
 }
 
-// Page contents through the host in the logical layout [hkv][page_size][128], converted
-// from / to the arena's block order (k_offset, v_offset).
+// Page contents through the host in the logical layout [hkv][page_size][128]; K is
+// converted from / to the arena's block order (k_offset).
 static int page_io(yx_ctx* c, yx_kv* kv, size_t layer, const uint32_t* pages, size_t n, void* k,
                    void* v, bool read) {
   if (!c || !kv || layer >= kv->layers) return fail(YX_ERR_INVALID, "bad arena or layer");
@@ -666,38 +666,41 @@ static int page_io(yx_ctx* c, yx_kv* kv, size_t layer, const uint32_t* pages, si
   const size_t pb = kv->page_bytes();
   const size_t ph = pb / 2;  // halves per page
   std::vector<uint16_t> tmp(ph);
-  // Arena offset of logical element (h, off, d) of one page.
-  auto arena_at = [&](bool is_k, size_t h, uint32_t off, uint32_t d) {
-    const size_t region = h * kv->page * 128;
-    return region + (is_k ? yx::k_offset(off, d / 8) + d % 8 : yx::v_offset(off, d));
-  };
-  auto permute = [&](bool is_k, uint16_t* logical, uint16_t* arena, bool to_arena) {
+  auto permute = [&](const uint16_t* logical, uint16_t* arena, bool to_arena) {
     for (size_t h = 0; h < kv->hkv; ++h)
       for (uint32_t off = 0; off < kv->page; ++off)
-        for (uint32_t d = 0; d < 128; ++d) {
-          uint16_t* l = logical + (h * kv->page + off) * 128 + d;
-          uint16_t* a = arena + arena_at(is_k, h, off, d);
-          if (to_arena) *a = *l;
-          else *l = *a;
+        for (uint32_t ch = 0; ch < 16; ++ch) {
+          const size_t region = h * kv->page * 128;
+          const uint16_t* src;
+          uint16_t* dst;
+          if (to_arena) {
+            src = logical + region + off * 128 + ch * 8;
+            dst = arena + region + yx::k_offset(off, ch);
+          } else {
+            src = arena + region + yx::k_offset(off, ch);
+            dst = const_cast<uint16_t*>(logical) + region + off * 128 + ch * 8;
+          }
+          std::memcpy(dst, src, 16);
         }
   };
   for (size_t i = 0; i < n; ++i) {
     if (pages[i] >= kv->pages) return fail(YX_ERR_INVALID, "page beyond the arena");
-    for (int part = 0; part < 2; ++part) {
-      const bool is_k = part == 0;
-      void* host = is_k ? k : v;
-      if (!host) continue;
-      char* dev = reinterpret_cast<char*>(is_k ? kv->k[layer] : kv->v[layer]) + pages[i] * pb;
-      uint16_t* logical = reinterpret_cast<uint16_t*>(static_cast<char*>(host) + i * pb);
-      if (read) {
-        YX_HIP(hipMemcpyAsync(tmp.data(), dev, pb, hipMemcpyDeviceToHost, c->stream));
+    char* kd = reinterpret_cast<char*>(kv->k[layer]) + pages[i] * pb;
+    char* vd = reinterpret_cast<char*>(kv->v[layer]) + pages[i] * pb;
+    if (read) {
+      if (k) {
+        YX_HIP(hipMemcpyAsync(tmp.data(), kd, pb, hipMemcpyDeviceToHost, c->stream));
         YX_HIP(hipStreamSynchronize(c->stream));
-        permute(is_k, logical, tmp.data(), false);
-      } else {
-        permute(is_k, logical, tmp.data(), true);
-        YX_HIP(hipMemcpyAsync(dev, tmp.data(), pb, hipMemcpyHostToDevice, c->stream));
+        permute(reinterpret_cast<uint16_t*>(static_cast<char*>(k) + i * pb), tmp.data(), false);
+      }
+      if (v) YX_HIP(hipMemcpyAsync(static_cast<char*>(v) + i * pb, vd, pb, hipMemcpyDeviceToHost, c->stream));
+    } else {
+      if (k) {
+        permute(reinterpret_cast<const uint16_t*>(static_cast<const char*>(k) + i * pb), tmp.data(), true);
+        YX_HIP(hipMemcpyAsync(kd, tmp.data(), pb, hipMemcpyHostToDevice, c->stream));
         YX_HIP(hipStreamSynchronize(c->stream));
       }
+      if (v) YX_HIP(hipMemcpyAsync(vd, static_cast<const char*>(v) + i * pb, pb, hipMemcpyHostToDevice, c->stream));
     }
   }
   YX_HIP(hipStreamSynchronize(c->stream));
