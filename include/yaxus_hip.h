@@ -51,7 +51,8 @@ int yx_ctx_destroy(yx_ctx* ctx);
 int yx_sync(yx_ctx* ctx);
 /* Tuning knobs: "attn_target_waves" (waves the split-K work list aims at; 0, the
  * default, means one work item per CU), "attn_max_chunk_blocks" (most 16-key blocks per
- * work item), "attn_max_tiles" (most 8-row MFMA tiles a decode wave holds, 1-4),
+ * work item), "attn_max_tiles" (most 8-row MFMA tiles a decode wave holds, 1-4, default 3; a row's
+ * q heads always fit one work item),
  * "prefill_min_rows" (rows of one sequence from which the prefill kernel is used),
  * "attn_decode_shape" (0, the default: one-tile decode passes whose work items hold at
  * most 64 blocks use the kernel whose waves share a queue of blocks; 1: the kernel with

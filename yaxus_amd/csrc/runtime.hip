@@ -170,7 +170,7 @@ struct yx_ctx {
   int cus = 256;
   long max_chunk_blocks = 1 << 20;
   long prefill_min_rows = 32;
-  long max_tiles = 4;
+  long max_tiles = 3;  // a fourth tile does not fit one wave's registers (it spills)
   long decode_shape = 0;  // 0: balanced one-tile kernel where it applies, 1: static split only
   bool profiling = false;
   Profile prof[4];
@@ -266,6 +266,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   }
   size_t nt = (max_rows * G + 7) / 8;
   nt = std::max<size_t>(1, std::min<size_t>(nt, static_cast<size_t>(c->max_tiles)));
+  nt = std::max<size_t>(nt, (G + 7) / 8);  // one row's q heads always fit one work item
   const size_t rows_per_sub = nt * 8 / G;
   if (rows_per_sub == 0) return fail(YX_ERR_UNSUPPORTED, "more than 32 query heads per KV head");
 
@@ -298,7 +299,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   // One workgroup per CU runs at a time for every tile count (8 waves of ~220
   // registers, or 4 of more than 256), so by default the split aims at one work item
   // per CU: more would run in a second round.
-  const size_t waves = nt == 1 ? yx::DecodeWaves<1>::value : yx::DecodeWaves<4>::value;
+  const size_t waves = nt == 1 ? yx::DecodeWaves<1>::value : yx::DecodeWaves<2>::value;
   const size_t target_items = c->target_waves > 0
                                   ? std::max<size_t>(1, static_cast<size_t>(c->target_waves) / waves)
                                   : static_cast<size_t>(c->cus);
@@ -439,7 +440,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     case 1: YX_LAUNCH_DECODE(1); break;
     case 2: YX_LAUNCH_DECODE(2); break;
     case 3: YX_LAUNCH_DECODE(3); break;
-    default: YX_LAUNCH_DECODE(4); break;
+    default: YX_LAUNCH_DECODE(4); break;  // only when one row has more than 24 q heads
   }
 #undef YX_LAUNCH_DECODE
   YX_HIP(hipGetLastError());
