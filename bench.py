@@ -179,6 +179,45 @@ def _time_write_rows(hip, kv, pr, layers, steps):
     return us, rows * (cols * 4 + HQ * D * 4 + HKV * D * 2 * 2)
 
 
+def _time_backend_attention(hip, kv, pr, layers, steps):
+    """Backend::attention in full (write_rows then attend) per layer for the pass `pr`,
+    device inputs: (us one launch, us as write_rows + attention launches)."""
+    from yaxus_amd.rope import inv_freq, rope_table
+
+    rows = len(pr.meta.pos)
+    cols = (HQ + 2 * HKV) * D
+    qkv = hip.tensor((rows, cols))
+    hip.fill_normal(qkv.ptr, rows * cols, False, SEED + 81, 0)
+    qn, kn = hip.tensor((D,)), hip.tensor((D,))
+    hip.fill_normal(qn.ptr, D, False, SEED + 82, 0)
+    hip.fill_normal(kn.ptr, D, False, SEED + 83, 0)
+    table = rope_table(inv_freq(D, 10000.0), 1.0, int(max(pr.meta.pos)) + 1)
+    cs = hip.tensor(table.shape).upload(table)
+    q, out = hip.tensor((rows, HQ * D)), hip.tensor((rows, HQ * D))
+    hip.begin_pass(pr.meta)
+
+    def one():
+        for l in range(layers):
+            hip.attention(kv, l, qkv, qn, kn, cs, 1e-6, HQ, out=out)
+
+    def two():
+        for l in range(layers):
+            hip.qk_rope_append(kv, l, qkv, qn, kn, cs, 1e-6, HQ, out=q)
+            hip.attend(kv, l, q, HQ, out=out)
+
+    res = []
+    for fn in (one, two):
+        fn()
+        hip.sync()
+        hip.timer_start()
+        for _ in range(steps):
+            fn()
+        res.append(hip.timer_stop() * 1000.0 / (steps * layers))
+    for t in (qkv, qn, kn, cs, q, out):
+        t.free()
+    return res
+
+
 def bench_configs(hip, steps=10, include_long=True):
     """BASELINE configurations 2-5 at full size (one JSON object per configuration)."""
     from yaxus_amd import KvCache
@@ -204,7 +243,10 @@ def bench_configs(hip, steps=10, include_long=True):
     logical = sum(ctx) * HKV * D * 2 * 2
     unique = (1024 + int(sum(suf)) + B) * HKV * D * 2 * 2
     wr_us, wr_bytes = _time_write_rows(hip, kv, pr, layers, steps)
+    ba_one, ba_two = _time_backend_attention(hip, kv, pr, layers, steps)
     res["cfg2_prefix_decode"] = {"us_per_layer_step": round(us, 2),
+                                 "backend_attention_us_one_launch": round(ba_one, 2),
+                                 "backend_attention_us_two_launches": round(ba_two, 2),
                                  "logical_GBs": round(logical / us / 1e3, 1),
                                  "unique_GBs": round(unique / us / 1e3, 1),
                                  "logical_bytes": logical, "unique_bytes": unique,

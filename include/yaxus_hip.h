@@ -6,10 +6,10 @@
  *   Backend::new_kv      (lib.rs:118)  -> yx_kv_create
  *   Backend::copy_page   (lib.rs:120)  -> yx_kv_copy_pages (a batch of PageCopy, kv.rs:35)
  *   Backend::begin_pass  (lib.rs:123)  -> yx_pass_begin    (PassMeta, lib.rs:63-89)
- *   Backend::attention   (lib.rs:132)  -> yx_qk_rope_append_dev (write_rows, backend-cpu
- *                                          lib.rs:359-385: q/k RMSNorm + RoPE, K/V store)
- *                                          + yx_attention (attend, lib.rs:389-427); or
- *                                          yx_kv_append for the K/V store alone
+ *   Backend::attention   (lib.rs:132)  -> yx_attention_qkv_dev (write_rows, backend-cpu
+ *                                          lib.rs:359-385, then attend, lib.rs:389-427);
+ *                                          or its halves: yx_qk_rope_append_dev and
+ *                                          yx_attention_dev; yx_kv_append stores K/V alone
  *
  * Conventions: int status, YX_OK = 0 (codes shared with yaxus_kv_cache.h);
  * yx_last_error() returns a thread-local message; no exception crosses the ABI. Every
@@ -102,6 +102,17 @@ int yx_kv_append_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k, const
 int yx_qk_rope_append_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* qkv,
                           const float* q_norm, const float* k_norm, const float* rope_cs,
                           size_t rope_len, float eps, size_t hq, size_t hkv, float* q_out);
+
+/* Backend::attention in full (lib.rs:132; backend-cpu lib.rs:516-530: write_rows then
+ * attend), device pointers, arguments as yx_qk_rope_append_dev and yx_attention_dev.
+ * One launch when the pass is a one-tile decode pass (each group's rows in one work
+ * item chain): the attention kernel normalises and rotates its rows' q heads into LDS
+ * and the group's last work item stores the rows' K/V, with write_rows' bits; otherwise
+ * write_rows runs as its own launch first. out `[rows][hq * 128]` f32. */
+int yx_attention_qkv_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* qkv,
+                         const float* q_norm, const float* k_norm, const float* rope_cs,
+                         size_t rope_len, float eps, float* out, size_t hq, size_t hkv,
+                         size_t window, float scale);
 
 /* attend (backend-cpu lib.rs:389-427; ATTN_SPLIT + ATTN_COMBINE, shaders.rs:1466-1637):
  * causal GQA attention of q `[rows][hq][128]` f32 over each row's keys `[lo, pos]`,

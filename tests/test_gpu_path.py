@@ -297,3 +297,49 @@ def test_model_attention_two_passes_across_pages(hip, window):
         ok, ov = orc.page_bits(p)
         assert np.array_equal(k[i], ok) and np.array_equal(v[i], ov)
     kv.destroy()
+
+
+@pytest.mark.parametrize("hq,hkv,lens,k", [
+    (16, 4, [1, 300, 17, 1000, 64], 1), (8, 2, [40, 513], 1), (16, 4, [40, 513, 7], 5),
+    (32, 2, [100, 2000], 1)])
+def test_attention_in_one_launch_equals_two(hip, hq, hkv, lens, k):
+    """Backend::attention in full: the decode kernel that runs write_rows itself gives the
+    same bits (attention output and stored K/V) as write_rows then attention in two
+    launches, and both match the oracle. Verify passes (k > 1) take the two-launch path."""
+    from yaxus_amd.rope import inv_freq, rope_table
+
+    f = inv_freq(D, 10000.0)
+    table = rope_table(f, 1.0, 4096)
+    outs, scs = [], []
+    for one_launch in (True, False):
+        sc = Scenario(hip, pages=400, page=16, hkv=hkv, pool_seed=21)
+        seqs = [sc.cache.new_seq() for _ in lens]
+        sc.prefill(dict(zip(seqs, lens)))
+        pr = sc.run_pass([(s, k) for s in seqs])
+        rows = len(pr.meta.pos)
+        qkv = sc.draw(rows * (hq + 2 * hkv) * D).reshape(rows, -1)
+        qn, kn = sc.draw(D) * 0.1, sc.draw(D) * 0.1
+        if one_launch:
+            got = hip.attention(sc.kv, 0, qkv, qn, kn, table, 1e-6, hq)
+        else:
+            q = hip.qk_rope_append(sc.kv, 0, qkv, qn, kn, table, 1e-6, hq)
+            got = hip.attend(sc.kv, 0, q, hq)
+        outs.append(got)
+        scs.append((sc, pr))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    (sa, pr), (sb, _) = scs
+    written = sorted(set(int(s) // 16 for s in pr.meta.kv_slot))
+    ka, va = sa.kv.read_pages(0, written)
+    kb, vb = sb.kv.read_pages(0, written)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    # The oracle on a third, identical scenario (same seeds, so the same inputs).
+    rows = len(pr.meta.pos)
+    sc = Scenario(hip, pages=400, page=16, hkv=hkv, pool_seed=21)
+    seqs = [sc.cache.new_seq() for _ in lens]
+    sc.prefill(dict(zip(seqs, lens)))
+    pr = sc.run_pass([(s, k) for s in seqs])
+    qkv = sc.draw(rows * (hq + 2 * hkv) * D).reshape(rows, -1)
+    qn, kn = sc.draw(D) * 0.1, sc.draw(D) * 0.1
+    qo = sc.orc[0].write_rows(qkv, hq, qn, kn, 1e-6, f, 1.0, pr.meta.pos, pr.meta.kv_slot)
+    want = sc.orc[0].attend(qo, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
+    assert close(outs[0], want).all(), f"max abs err {np.abs(outs[0] - want).max()}"

@@ -83,6 +83,7 @@ HIP_SYMBOLS = {
     "yx_kv_append": (I, [P, P, S, P, P]),
     "yx_kv_append_dev": (I, [P, P, S, P, P]),
     "yx_qk_rope_append_dev": (I, [P, P, S, P, P, P, P, S, F, S, S, P]),
+    "yx_attention_qkv_dev": (I, [P, P, S, P, P, P, P, S, F, P, S, S, S, F]),
     "yx_attention": (I, [P, P, S, P, P, S, S, S, F]),
     "yx_attention_dev": (I, [P, P, S, P, P, S, S, S, F]),
     "yx_attention_append": (I, [P, P, S, P, P, P, P, S, S, S, F]),

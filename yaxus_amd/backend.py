@@ -189,17 +189,37 @@ class HipBackend:
                 t.free()
 
     # Backend::attention (lib.rs:132; backend-cpu lib.rs:516-530): write_rows, then attend
-    # the rows' queries. Device tensors stay on the device (no synchronisation).
+    # the rows' queries (one launch for decode passes). Device tensors stay on the
+    # device (no synchronisation); numpy arrays go through temporaries.
     def attention(self, kv, layer, qkv, q_norm, k_norm, rope_cs, eps, hq, window=None,
                   scale=None, out=None):
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(kv.d))) if scale is None else scale
+        w = int(window or 0)
+        rope_len = int(rope_cs.shape[1]) if len(rope_cs.shape) == 3 else int(rope_cs.shape[0]) // 2
         if isinstance(qkv, DeviceTensor):
-            q = self.qk_rope_append(kv, layer, qkv, q_norm, k_norm, rope_cs, eps, hq)
+            out = out if out is not None else self.tensor((self.rows, hq * kv.d))
+            check_hip(self.L.yx_attention_qkv_dev(self.ctx, kv.h, layer, qkv.ptr, q_norm.ptr,
+                                                  k_norm.ptr, rope_cs.ptr, rope_len, float(eps),
+                                                  out.ptr, hq, kv.hkv, w, scale))
+            return out
+        qkv = np.ascontiguousarray(qkv, np.float32)
+        if qkv.size != self.rows * (hq + 2 * kv.hkv) * kv.d:
+            raise ValueError("qkv must be [rows][(hq + 2 hkv) * head_dim] f32")
+        arrays = (qkv, q_norm, k_norm, rope_cs)
+        tmp = [self.tensor(np.shape(a)) for a in arrays]
+        try:
+            for t, a in zip(tmp, arrays):
+                t.upload(np.ascontiguousarray(a, np.float32))
+            o = self.tensor((self.rows, hq * kv.d))
             try:
-                return self.attend(kv, layer, q, hq, window=window, scale=scale, out=out)
+                self.attention(kv, layer, tmp[0], tmp[1], tmp[2], tmp[3], eps, hq, window=window,
+                               scale=scale, out=o)
+                return o.numpy()
             finally:
-                q.free()
-        q = self.qk_rope_append(kv, layer, qkv, q_norm, k_norm, rope_cs, eps, hq)
-        return self.attend(kv, layer, q, hq, window=window, scale=scale)
+                o.free()
+        finally:
+            for t in tmp:
+                t.free()
 
     # The attend half of Backend::attention (backend-cpu lib.rs:389-427)
     def attend(self, kv, layer, q, hq, window=None, scale=None, out=None):

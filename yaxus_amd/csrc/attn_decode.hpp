@@ -29,6 +29,7 @@
 #include <stdint.h>
 
 #include "kv_kernels.hpp"
+#include "qk_rope.hpp"
 
 namespace yx {
 
@@ -511,6 +512,8 @@ struct BalancedShared {
   float m[kBalQuads][8];
   float l[kBalQuads][8];
   float4 o[kBalQuads][8][kD / 4];
+  float q[8][kD];            // the item's queries when the kernel normalises and rotates them
+  float qsq[kBalWaves][kD];  // per-wave scratch of that step
   uint32_t next;
   uint32_t last;
 };
@@ -531,6 +534,22 @@ __device__ __forceinline__ void load_block_buf(BlockRegs& r, const _Float16* kbl
     r.v[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, ((4 * g + i) * kD + c * 8) * 2, 0, kNontemporal));
 }
 
+// The inputs of write_rows when the kernel runs it itself (Backend::attention in one
+// launch): the rows' projected qkv, the norm weights and the layer's RoPE table.
+struct QkvIn {
+  const float* qkv;
+  const float* q_norm;
+  const float* k_norm;
+  const float* rope_cs;
+  uint32_t rope_len;
+  float eps;
+};
+
+// QKV: instead of reading q (and storing knew/vnew), the workgroup normalises and rotates
+// its rows' q heads from qkv into LDS (write_rows' arithmetic, the same bits), and the
+// item of the group's last chunk normalises, rotates and stores the rows' key heads and
+// stores their value heads, before any wave reads a block.
+template <bool QKV>
 __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
     const AttnItem* __restrict__ items, const uint32_t* pos,
     const uint32_t* __restrict__ pages, const _Float16* kc, const _Float16* vc,
@@ -539,7 +558,7 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
     const float* __restrict__ knew, const float* __restrict__ vnew,
     const uint32_t* __restrict__ kv_slot, _Float16* kw, _Float16* vw,  // kw/vw alias kc/vc
     uint32_t part_o_bytes, uint32_t part_ml_bytes, uint32_t hq, uint32_t hkv,
-    uint32_t bpp_shift, uint32_t window, float scale_log2) {
+    uint32_t bpp_shift, uint32_t window, float scale_log2, QkvIn qi_in) {
   __shared__ BalancedShared sh;
   const AttnItem it = items[blockIdx.x];
   const uint32_t kh = blockIdx.y;
@@ -551,10 +570,35 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
   const uint32_t nlog = it.nrows * G;  // logical rows in the group (at most 8)
 
   if (threadIdx.x == 0) sh.next = kBalWaves;  // quads 0..W-1 go to waves 0..W-1
-  if (knew != nullptr && it.chunk == it.nch - 1)
-    fused_append<64 * kBalWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
-  else
+  if constexpr (QKV) {
+    // Wave t: logical row t's query head, then (last chunk only) row t - nlog's key head.
+    const uint32_t nk = it.chunk == it.nch - 1 ? it.nrows : 0;
+    const uint32_t qd = hq * kD, kvd = hkv * kD, cols = qd + 2 * kvd;
+    for (uint32_t t = static_cast<uint32_t>(wave); t < nlog + nk; t += kBalWaves) {
+      float o0, o1;
+      if (t < nlog) {
+        const uint32_t rr = it.r0 + t / G, h = kh * G + t % G;
+        norm_rope_head(qi_in.qkv + static_cast<size_t>(rr) * cols + h * kD, qi_in.q_norm,
+                       qi_in.rope_cs, qi_in.rope_len, pos[rr], qi_in.eps, lane, sh.qsq[wave], o0, o1);
+        sh.q[t][lane] = o0;
+        sh.q[t][lane + 64] = o1;
+      } else {
+        const uint32_t rr = it.r0 + (t - nlog);
+        const float* ks = qi_in.qkv + static_cast<size_t>(rr) * cols + qd + kh * kD;
+        norm_rope_head(ks, qi_in.k_norm, qi_in.rope_cs, qi_in.rope_len, pos[rr], qi_in.eps, lane,
+                       sh.qsq[wave], o0, o1);
+        store_kv_head(o0, o1, ks + kvd, kv_slot[rr], kh, hkv, 16u << bpp_shift, lane, kw, vw);
+      }
+    }
+    // Stores complete, then the barrier orders them (and the queries in LDS) before
+    // every wave's reads.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+  } else if (knew != nullptr && it.chunk == it.nch - 1) {
+    fused_append<64 * kBalWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
+  } else {
+    __syncthreads();
+  }
 
   const uint32_t nall = it.blk1 - it.blk0;  // at most 4 * kBalQuads (host-checked)
   const uint32_t nq = (nall + 3) / 4;
@@ -590,7 +634,7 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
   const int rlo = (window > 0 && p0 + 1 > static_cast<int>(window)) ? p0 + 1 - static_cast<int>(window) : 0;
   float4 qraw[8];
   {
-    const float* qp = q + (static_cast<size_t>(rr0) * hq + h0) * kD + g * 8;
+    const float* qp = QKV ? &sh.q[lr0][g * 8] : q + (static_cast<size_t>(rr0) * hq + h0) * kD + g * 8;
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
       qraw[2 * pp] = *reinterpret_cast<const float4*>(qp + pp * 32);

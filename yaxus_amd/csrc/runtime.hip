@@ -164,7 +164,7 @@ struct yx_ctx {
   bool have_pass = false;
   std::map<std::tuple<size_t, size_t, size_t>, AttnPlan> plans;
   // scratch
-  DevBuf part_o, part_ml, counters, io_a, io_b, io_c;
+  DevBuf part_o, part_ml, counters, io_a, io_b, io_c, io_q;
   // options
   long target_waves = 0;  // 0: one work item per CU
   int cus = 256;
@@ -369,11 +369,15 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
 
 int append_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v);
 
+int qk_rope_impl(yx_ctx* c, yx_kv* kv, size_t layer, const yx::QkvIn& in, size_t hq, float* q_out);
+
 // Attention of the pass's rows; with knew/vnew, the rows' K/V are stored first (in
-// the same kernel when the plan allows it, else by the append kernel before it).
+// the same kernel when the plan allows it, else by the append kernel before it); with
+// qkv, write_rows runs first (in the same kernel when the plan allows it, else as its
+// own launch into a scratch q).
 int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* out, size_t hq,
                    size_t hkv, size_t window, float scale, const float* knew = nullptr,
-                   const float* vnew = nullptr) {
+                   const float* vnew = nullptr, const yx::QkvIn* qkv = nullptr) {
   int rc = check_kv(c, kv, layer);
   if (rc) return rc;
   if (hkv != kv->hkv) return fail(YX_ERR_INVALID, "hkv differs from the arena's");
@@ -393,6 +397,12 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   if (knew && (plan->prefill || !plan->fusable)) {
     if ((rc = append_impl(c, kv, layer, knew, vnew))) return rc;
     knew = vnew = nullptr;
+  }
+  if (qkv && !(plan->balanced && plan->fusable)) {
+    if ((rc = c->io_q.ensure(std::max<size_t>(16, c->rows * hq * 128 * 4), c->stream))) return rc;
+    if ((rc = qk_rope_impl(c, kv, layer, *qkv, hq, static_cast<float*>(c->io_q.p)))) return rc;
+    q = static_cast<const float*>(c->io_q.p);
+    qkv = nullptr;
   }
   if (plan->prefill) {
     uint32_t shift = 0;
@@ -432,10 +442,17 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
                      static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],       \
                      po_bytes, pml_bytes, H, HK, P, W, scale_log2)
   if (plan->balanced) {
-    hipLaunchKernelGGL(yx::paged_attn_decode_balanced, grid, dim3(64 * yx::kBalWaves), 0, c->stream,
-                       items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml, cnt, knew, vnew,
-                       static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],
-                       po_bytes, pml_bytes, H, HK, P, W, scale_log2);
+    if (qkv)
+      hipLaunchKernelGGL(yx::paged_attn_decode_balanced<true>, grid, dim3(64 * yx::kBalWaves), 0,
+                         c->stream, items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml,
+                         cnt, nullptr, nullptr, static_cast<const uint32_t*>(c->d_slot.p),
+                         kv->k[layer], kv->v[layer], po_bytes, pml_bytes, H, HK, P, W, scale_log2,
+                         *qkv);
+    else
+      hipLaunchKernelGGL(yx::paged_attn_decode_balanced<false>, grid, dim3(64 * yx::kBalWaves), 0,
+                         c->stream, items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml,
+                         cnt, knew, vnew, static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer],
+                         kv->v[layer], po_bytes, pml_bytes, H, HK, P, W, scale_log2, yx::QkvIn{});
   } else switch (plan->nt) {
     case 1: YX_LAUNCH_DECODE(1); break;
     case 2: YX_LAUNCH_DECODE(2); break;
@@ -461,6 +478,36 @@ int append_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float*
                      static_cast<uint32_t>(kv->page));
   YX_HIP(hipGetLastError());
   return prof_end(c, YX_KERNEL_APPEND, e0);
+}
+
+// Rows of the pass that write_rows can run on: positions inside the RoPE table and
+// covered by their page tables.
+int check_qkv_rows(yx_ctx* c, yx_kv* kv, size_t rope_len) {
+  if (rope_len > 0xffffffffu) return fail(YX_ERR_UNSUPPORTED, "RoPE table too long");
+  for (size_t i = 0; i < c->rows; ++i) {
+    if (c->pos[i] >= rope_len) return fail(YX_ERR_INVALID, "a row's position is beyond the RoPE table");
+    if ((c->pos[i] / kv->page) + c->pt_off[i] >= c->npages)
+      return fail(YX_ERR_INVALID, "a row's position has no page-table entry");
+  }
+  return YX_OK;
+}
+
+// write_rows on its own: one wave per (row, head).
+int qk_rope_impl(yx_ctx* c, yx_kv* kv, size_t layer, const yx::QkvIn& in, size_t hq, float* q_out) {
+  if (c->rows == 0) return YX_OK;
+  const size_t hkv = kv->hkv;
+  dim3 grid(static_cast<unsigned>(c->rows),
+            static_cast<unsigned>((hq + hkv + yx::kRopeWaves - 1) / yx::kRopeWaves));
+  hipEvent_t e0;
+  int rc;
+  if ((rc = prof_begin(c, YX_KERNEL_QK_ROPE, &e0))) return rc;
+  hipLaunchKernelGGL(yx::qk_norm_rope_append, grid, dim3(64 * yx::kRopeWaves), 0, c->stream, in.qkv,
+                     in.q_norm, in.k_norm, in.rope_cs, in.rope_len, in.eps,
+                     static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_slot.p),
+                     kv->k[layer], kv->v[layer], q_out, static_cast<uint32_t>(hq),
+                     static_cast<uint32_t>(hkv), static_cast<uint32_t>(kv->page));
+  YX_HIP(hipGetLastError());
+  return prof_end(c, YX_KERNEL_QK_ROPE, e0);
 }
 
 }  // namespace
@@ -509,7 +556,7 @@ int yx_ctx_destroy(yx_ctx* c) {
     }
   for (auto& kv : c->plans) kv.second.d_items.release();
   for (DevBuf* b : {&c->d_pos, &c->d_slot, &c->d_pages, &c->part_o, &c->part_ml, &c->counters,
-                    &c->io_a, &c->io_b, &c->io_c})
+                    &c->io_a, &c->io_b, &c->io_c, &c->io_q})
     b->release();
   if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
   if (c->graph) (void)hipGraphDestroy(c->graph);
@@ -790,24 +837,23 @@ int yx_qk_rope_append_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* qkv,
   if ((rc = check_kv(c, kv, layer))) return rc;
   if (hkv != kv->hkv) return fail(YX_ERR_INVALID, "hkv differs from the arena's");
   if (hq == 0 || hq % hkv != 0) return fail(YX_ERR_INVALID, "hq must be a positive multiple of hkv");
-  if (c->rows == 0) return YX_OK;
-  for (size_t i = 0; i < c->rows; ++i) {
-    if (c->pos[i] >= rope_len) return fail(YX_ERR_INVALID, "a row's position is beyond the RoPE table");
-    if ((c->pos[i] / kv->page) + c->pt_off[i] >= c->npages)
-      return fail(YX_ERR_INVALID, "a row's position has no page-table entry");
-  }
-  if (rope_len > 0xffffffffu) return fail(YX_ERR_UNSUPPORTED, "RoPE table too long");
-  dim3 grid(static_cast<unsigned>(c->rows),
-            static_cast<unsigned>((hq + hkv + yx::kRopeWaves - 1) / yx::kRopeWaves));
-  hipEvent_t e0;
-  if ((rc = prof_begin(c, YX_KERNEL_QK_ROPE, &e0))) return rc;
-  hipLaunchKernelGGL(yx::qk_norm_rope_append, grid, dim3(64 * yx::kRopeWaves), 0, c->stream, qkv,
-                     q_norm, k_norm, rope_cs, static_cast<uint32_t>(rope_len), eps,
-                     static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_slot.p),
-                     kv->k[layer], kv->v[layer], q_out, static_cast<uint32_t>(hq),
-                     static_cast<uint32_t>(hkv), static_cast<uint32_t>(kv->page));
-  YX_HIP(hipGetLastError());
-  return prof_end(c, YX_KERNEL_QK_ROPE, e0);
+  if ((rc = check_qkv_rows(c, kv, rope_len))) return rc;
+  const yx::QkvIn in{qkv, q_norm, k_norm, rope_cs, static_cast<uint32_t>(rope_len), eps};
+  return qk_rope_impl(c, kv, layer, in, hq, q_out);
+}
+
+int yx_attention_qkv_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* qkv,
+                         const float* q_norm, const float* k_norm, const float* rope_cs,
+                         size_t rope_len, float eps, float* out, size_t hq, size_t hkv,
+                         size_t window, float scale) {
+  if (!c || !kv || !qkv || !q_norm || !k_norm || !rope_cs || !out)
+    return fail(YX_ERR_INVALID, "null argument");
+  int rc = c->set_device();
+  if (rc) return rc;
+  if ((rc = check_kv(c, kv, layer))) return rc;
+  if ((rc = check_qkv_rows(c, kv, rope_len))) return rc;
+  const yx::QkvIn in{qkv, q_norm, k_norm, rope_cs, static_cast<uint32_t>(rope_len), eps};
+  return attention_impl(c, kv, layer, nullptr, out, hq, hkv, window, scale, nullptr, nullptr, &in);
 }
 
 int yx_kv_append(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v) {
