@@ -1,0 +1,138 @@
+// A decode serving loop driven through the C ABIs alone (no Python): the host
+// allocator appends one token per sequence, the pass goes to the device, and every layer
+// stores the new K/V and attends in one launch; the step ends with yx_sync, as a
+// native engine would run it (crates/yaxus-model/src/engine/mod.rs:530-551 over
+// Model::forward, crates/yaxus-model/src/lib.rs:434-453). Prints one JSON line:
+// host time per step (allocator + pass upload), whole-step time, and device time for
+// the attention launches alone.
+//
+// Usage: decode_loop [steps] [batch] [context] [layers]
+#include <algorithm>
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+#include "../../include/yaxus_hip.h"
+#include "../../include/yaxus_kv_cache.h"
+
+namespace {
+
+void die(const char* what, const char* msg) {
+  std::fprintf(stderr, "%s: %s\n", what, msg);
+  std::exit(1);
+}
+#define HIPCHECK(x) \
+  do {              \
+    if ((x) != YX_OK) die(#x, yx_last_error()); \
+  } while (0)
+#define KVCHECK(x) \
+  do {             \
+    if ((x) != YX_OK) die(#x, yx_cache_last_error()); \
+  } while (0)
+
+double median(std::vector<double> v) {
+  std::sort(v.begin(), v.end());
+  return v.empty() ? 0.0 : v[v.size() / 2];
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const int steps = argc > 1 ? std::atoi(argv[1]) : 20;
+  const size_t B = argc > 2 ? std::strtoul(argv[2], nullptr, 10) : 16;
+  const size_t ctx_len = argc > 3 ? std::strtoul(argv[3], nullptr, 10) : 4000;
+  const size_t layers = argc > 4 ? std::strtoul(argv[4], nullptr, 10) : 24;
+  const size_t page = 16, hq = 16, hkv = 4, d = 128;
+  const size_t pages = B * ((ctx_len + steps) / page + 2) + 16;
+
+  yx_cache* cache = nullptr;
+  KVCHECK(yx_cache_create(pages, 1 << 20, page, &cache));
+  std::vector<uint64_t> seqs(B);
+  for (auto& s : seqs) s = yx_cache_new_seq(cache);
+  {
+    std::vector<size_t> counts(B, ctx_len);
+    std::vector<uint32_t> toks(B * ctx_len, 1);
+    KVCHECK(yx_cache_append(cache, B, seqs.data(), counts.data(), toks.data()));
+  }
+
+  yx_ctx* ctx = nullptr;
+  HIPCHECK(yx_ctx_create(0, &ctx));
+  yx_kv* kv = nullptr;
+  HIPCHECK(yx_kv_create(ctx, layers, pages, page, hkv, d, YX_DTYPE_F16, &kv));
+  const size_t per_arena = pages * yx_kv_page_bytes(kv) / 2;
+  for (size_t l = 0; l < layers; ++l)
+    for (int part = 0; part < 2; ++part) {
+      void* p = nullptr;
+      HIPCHECK(yx_kv_layer_ptr(kv, l, part, &p));
+      HIPCHECK(yx_fill_normal(ctx, p, per_arena, YX_DTYPE_F16, 0x59415855ull, (2 * l + part) * per_arena));
+    }
+  void *q, *k, *v, *out;
+  HIPCHECK(yx_dev_alloc(ctx, B * hq * d * 4, &q));
+  HIPCHECK(yx_dev_alloc(ctx, B * hkv * d * 4, &k));
+  HIPCHECK(yx_dev_alloc(ctx, B * hkv * d * 4, &v));
+  HIPCHECK(yx_dev_alloc(ctx, B * hq * d * 4, &out));
+  HIPCHECK(yx_fill_normal(ctx, q, B * hq * d, YX_DTYPE_F32, 7, 0));
+  HIPCHECK(yx_fill_normal(ctx, k, B * hkv * d, YX_DTYPE_F32, 7, 1ull << 32));
+  HIPCHECK(yx_fill_normal(ctx, v, B * hkv * d, YX_DTYPE_F32, 7, 2ull << 32));
+  HIPCHECK(yx_sync(ctx));
+
+  const float scale = 0.08838834764831845f;  // 1 / sqrt(128)
+  std::vector<size_t> ones(B, 1);
+  std::vector<uint32_t> tok(B, 2);
+  std::vector<uint32_t> ids, pos, slot, pt_off, pg;
+  std::vector<size_t> last;
+  std::vector<yx_page_copy> copies;
+  std::vector<uint32_t> src, dst;
+  std::vector<double> host_us, step_us;
+  using clk = std::chrono::steady_clock;
+  for (int it = 0; it < steps + 3; ++it) {
+    const auto t0 = clk::now();
+    KVCHECK(yx_cache_append(cache, B, seqs.data(), ones.data(), tok.data()));
+    copies.resize(yx_cache_pending_copies(cache));
+    copies.resize(yx_cache_take_copies(cache, copies.data(), copies.size()));
+    if (!copies.empty()) {
+      src.clear();
+      dst.clear();
+      for (const auto& c : copies) {
+        src.push_back(c.src);
+        dst.push_back(c.dst);
+      }
+      HIPCHECK(yx_kv_copy_pages(ctx, kv, src.data(), dst.data(), src.size()));
+    }
+    const size_t rows = yx_cache_pass_rows(cache), np = yx_cache_pass_npages(cache);
+    ids.resize(rows);
+    pos.resize(rows);
+    slot.resize(rows);
+    pt_off.resize(rows);
+    pg.resize(np);
+    last.resize(yx_cache_pass_nitems(cache));
+    yx_cache_pass_get(cache, ids.data(), pos.data(), slot.data(), pt_off.data(), pg.data(), last.data());
+    HIPCHECK(yx_pass_begin(ctx, rows, pos.data(), slot.data(), pt_off.data(), pg.data(), np));
+    const auto t1 = clk::now();
+    for (size_t l = 0; l < layers; ++l)
+      HIPCHECK(yx_attention_append_dev(ctx, kv, l, static_cast<float*>(k), static_cast<float*>(v),
+                                       static_cast<float*>(q), static_cast<float*>(out), hq, hkv, 0,
+                                       scale));
+    HIPCHECK(yx_sync(ctx));
+    const auto t2 = clk::now();
+    if (it >= 3) {
+      host_us.push_back(std::chrono::duration<double, std::micro>(t1 - t0).count());
+      step_us.push_back(std::chrono::duration<double, std::micro>(t2 - t0).count());
+    }
+  }
+  float ms = 0;
+  HIPCHECK(yx_timer_start(ctx));
+  for (size_t l = 0; l < layers; ++l)
+    HIPCHECK(yx_attention_append_dev(ctx, kv, l, static_cast<float*>(k), static_cast<float*>(v),
+                                     static_cast<float*>(q), static_cast<float*>(out), hq, hkv, 0, scale));
+  HIPCHECK(yx_timer_stop(ctx, &ms));
+  std::printf("{\"batch\": %zu, \"context\": %zu, \"layers\": %zu, \"host_us_median\": %.1f, "
+              "\"step_us_median\": %.1f, \"attention_us_all_layers\": %.1f}\n",
+              B, ctx_len, layers, median(host_us), median(step_us), ms * 1000.0);
+  for (void* p : {q, k, v, out}) yx_dev_free(ctx, p);
+  yx_kv_destroy(ctx, kv);
+  yx_ctx_destroy(ctx);
+  yx_cache_destroy(cache);
+  return 0;
+}

@@ -46,6 +46,16 @@ def build_hip():
     _run([HIPCC, *HIP_FLAGS, *srcs, "-o", HIP_LIB])
 
 
+NATIVE_LOOP = os.path.join(ROOT, "tests", "native", "decode_loop")
+
+
+def build_native_tests():
+    """The C++ decode loop over the C ABIs (tests/native), linked to the libraries above."""
+    _run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", NATIVE_LOOP + ".cpp",
+          "-L" + HERE, "-lyaxus_hip", "-lyaxus_kv", "-Wl,-rpath,$ORIGIN/../../yaxus_amd",
+          "-o", NATIVE_LOOP])
+
+
 def build_oracle():
     _run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "-B"])
 
@@ -53,6 +63,7 @@ def build_oracle():
 def build_all():
     build_kv()
     build_hip()
+    build_native_tests()
     build_oracle()
 
 
