@@ -70,7 +70,7 @@ class OracleModelBackend:
         return kv[layer].attend(q, hq, m.pos, m.pt_off, m.pages, window=window or 0)
 
 
-def run(backend, reqs, together):
+def run(backend, reqs, together, passes=None):
     model = PagedModel(backend, PAGES, max_pos=4096, page=PAGE, layers=LAYERS, hkv=HKV, hq=HQ,
                        windows=[0, 64], chunk=96)
     eng = Recording(model, EngineConfig(decode_rows=4, busy_prefill_rows=32), token_fn=token_fn)
@@ -82,6 +82,8 @@ def run(backend, reqs, together):
         for r in reqs:
             eng.submit(r)
             eng.run_all()
+    if passes is not None:
+        passes.extend(eng.passes)
     return eng.record
 
 
@@ -95,3 +97,24 @@ def test_concurrent_matches_solo_and_the_oracle(hip):
     for key in both:
         assert close(both[key], solo[key]).all(), key
         assert close(both[key], orc[key]).all(), key
+
+
+def test_speculative_matches_plain(hip):
+    """Reference vs_cpu.rs:124-160 `speculative_matches_plain`, at the attention level:
+    a request decoded with verify passes (hint proposals, some wrong, so rewinds happen)
+    ends with the same attention outputs per (position, layer) as plain decoding."""
+    f = lambda p: (p * 7 + 3) % 97 + 200  # the token the test model emits at position p
+    prompt = [(t * 13) % 90 + 1 for t in range(70)]
+    n_new = 12
+    good = [f(len(prompt) - 1 + i) for i in range(n_new)]
+    hint = list(good)
+    hint[4] = 5  # rejected: the verify pass rewinds to before it
+    hint[9] = 6
+    plain = run(hip, [Request(0, prompt, n_new)], together=False)
+    kinds = []
+    spec = run(hip, [Request(0, prompt, n_new, hint=hint)], together=False, passes=kinds)
+    verify = [n for kind, n in kinds if kind == "verify"]
+    assert len(verify) >= 2 and max(verify) > 1, kinds  # multi-row verify passes ran
+    assert set(plain) == set(spec)
+    for key in plain:
+        assert close(spec[key], plain[key]).all(), key
