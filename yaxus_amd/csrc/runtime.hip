@@ -211,6 +211,10 @@ int check_kv(yx_ctx* c, yx_kv* kv, size_t layer) {
     return fail(YX_ERR_INVALID, "a page table names a page beyond the arena");
   if (c->rows && c->max_slot >= kv->pages * kv->page)
     return fail(YX_ERR_INVALID, "a kv_slot lies beyond the arena");
+  // Every key a row can see (up to its position) must have a page-table entry.
+  for (size_t i = 0; i < c->rows; ++i)
+    if ((c->pos[i] / kv->page) + c->pt_off[i] >= c->npages)
+      return fail(YX_ERR_INVALID, "a row's position has no page-table entry");
   return YX_OK;
 }
 
@@ -480,15 +484,12 @@ int append_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float*
   return prof_end(c, YX_KERNEL_APPEND, e0);
 }
 
-// Rows of the pass that write_rows can run on: positions inside the RoPE table and
-// covered by their page tables.
-int check_qkv_rows(yx_ctx* c, yx_kv* kv, size_t rope_len) {
+// Rows of the pass that write_rows can run on: positions inside the RoPE table (the
+// page-table coverage is checked with the arena, check_kv).
+int check_qkv_rows(yx_ctx* c, size_t rope_len) {
   if (rope_len > 0xffffffffu) return fail(YX_ERR_UNSUPPORTED, "RoPE table too long");
-  for (size_t i = 0; i < c->rows; ++i) {
+  for (size_t i = 0; i < c->rows; ++i)
     if (c->pos[i] >= rope_len) return fail(YX_ERR_INVALID, "a row's position is beyond the RoPE table");
-    if ((c->pos[i] / kv->page) + c->pt_off[i] >= c->npages)
-      return fail(YX_ERR_INVALID, "a row's position has no page-table entry");
-  }
   return YX_OK;
 }
 
@@ -811,8 +812,6 @@ int yx_pass_begin(yx_ctx* c, size_t rows, const uint32_t* pos, const uint32_t* k
   if ((rc = st.upload(c->d_pos.p, pos, rows * 4, c->stream))) return rc;
   if ((rc = st.upload(c->d_slot.p, kv_slot, rows * 4, c->stream))) return rc;
   if ((rc = st.upload(c->d_pages.p, pages, npages * 4, c->stream))) return rc;
-  // Each row's last visible key must have a page-table entry.
-  for (size_t i = 0; i < rows; ++i) (void)i;
   c->have_pass = true;
   return YX_OK;
 }
@@ -821,9 +820,6 @@ int yx_kv_append_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const f
   if (!c) return fail(YX_ERR_INVALID, "null context");
   int rc = c->set_device();
   if (rc) return rc;
-  for (size_t i = 0; i < c->rows; ++i)
-    if ((c->pos[i] / kv->page) + c->pt_off[i] >= c->npages)
-      return fail(YX_ERR_INVALID, "a row's position has no page-table entry");
   return append_impl(c, kv, layer, k, v);
 }
 
@@ -837,7 +833,7 @@ int yx_qk_rope_append_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* qkv,
   if ((rc = check_kv(c, kv, layer))) return rc;
   if (hkv != kv->hkv) return fail(YX_ERR_INVALID, "hkv differs from the arena's");
   if (hq == 0 || hq % hkv != 0) return fail(YX_ERR_INVALID, "hq must be a positive multiple of hkv");
-  if ((rc = check_qkv_rows(c, kv, rope_len))) return rc;
+  if ((rc = check_qkv_rows(c, rope_len))) return rc;
   const yx::QkvIn in{qkv, q_norm, k_norm, rope_cs, static_cast<uint32_t>(rope_len), eps};
   return qk_rope_impl(c, kv, layer, in, hq, q_out);
 }
@@ -851,7 +847,7 @@ int yx_attention_qkv_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* qkv,
   int rc = c->set_device();
   if (rc) return rc;
   if ((rc = check_kv(c, kv, layer))) return rc;
-  if ((rc = check_qkv_rows(c, kv, rope_len))) return rc;
+  if ((rc = check_qkv_rows(c, rope_len))) return rc;
   const yx::QkvIn in{qkv, q_norm, k_norm, rope_cs, static_cast<uint32_t>(rope_len), eps};
   return attention_impl(c, kv, layer, nullptr, out, hq, hkv, window, scale, nullptr, nullptr, &in);
 }
@@ -876,10 +872,6 @@ int yx_attention_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* 
   if (!c) return fail(YX_ERR_INVALID, "null context");
   int rc = c->set_device();
   if (rc) return rc;
-  if (kv)
-    for (size_t i = 0; i < c->rows; ++i)
-      if ((c->pos[i] / kv->page) + c->pt_off[i] >= c->npages)
-        return fail(YX_ERR_INVALID, "a row's position has no page-table entry");
   return attention_impl(c, kv, layer, q, out, hq, hkv, window, scale);
 }
 
@@ -907,9 +899,6 @@ int yx_attention_append_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, 
   if (!k || !v) return fail(YX_ERR_INVALID, "null k or v");
   int rc = c->set_device();
   if (rc) return rc;
-  for (size_t i = 0; i < c->rows; ++i)
-    if ((c->pos[i] / kv->page) + c->pt_off[i] >= c->npages)
-      return fail(YX_ERR_INVALID, "a row's position has no page-table entry");
   return attention_impl(c, kv, layer, q, out, hq, hkv, window, scale, k, v);
 }
 
