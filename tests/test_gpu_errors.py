@@ -1,0 +1,65 @@
+"""Misuse of the device ABI is refused on the host with a status and a message, before
+any kernel is launched (the reference GPU backend panics on misuse, ops/attention.rs:28-36;
+here the status reaches the caller)."""
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+
+from yaxus_amd._lib import YxError
+
+pytestmark = pytest.mark.gpu
+D = 128
+
+
+def _meta(pos, slot, pt_off, pages):
+    return SimpleNamespace(pos=np.array(pos, np.uint32), kv_slot=np.array(slot, np.uint32),
+                           pt_off=np.array(pt_off, np.uint32), pages=np.array(pages, np.uint32))
+
+
+@pytest.fixture
+def kv(hip):
+    kv = hip.new_kv(1, 8, 16, 2)
+    yield kv
+    kv.destroy()
+
+
+def test_rejects_a_position_without_a_page_table_entry(hip, kv):
+    hip.begin_pass(_meta([40], [3 * 16 + 8], [0], [3]))  # position 40 needs 3 pages
+    with pytest.raises(YxError, match="page-table entry"):
+        hip.attend(kv, 0, np.zeros((1, 4 * D), np.float32), 4)
+
+
+def test_rejects_pages_beyond_the_arena(hip, kv):
+    hip.begin_pass(_meta([0], [0], [0], [8]))
+    with pytest.raises(YxError, match="beyond the arena"):
+        hip.attend(kv, 0, np.zeros((1, 4 * D), np.float32), 4)
+
+
+def test_rejects_head_counts_that_do_not_match(hip, kv):
+    hip.begin_pass(_meta([0], [0], [0], [1]))
+    with pytest.raises(YxError, match="multiple of hkv"):
+        hip.attend(kv, 0, np.zeros((1, 3 * D), np.float32), 3)
+
+
+def test_rejects_rows_of_one_sequence_that_are_not_consecutive(hip):
+    with pytest.raises(YxError, match="not consecutive"):
+        hip.begin_pass(_meta([0, 0, 1], [0, 16, 1], [0, 1, 0], [0, 1]))
+
+
+def test_rejects_a_layer_beyond_the_arena(hip, kv):
+    hip.begin_pass(_meta([0], [0], [0], [1]))
+    with pytest.raises(YxError, match="layer"):
+        hip.attend(kv, 3, np.zeros((1, 4 * D), np.float32), 4)
+
+
+def test_the_context_still_works_after_an_error(hip, kv):
+    hip.begin_pass(_meta([40], [3 * 16 + 8], [0], [3]))
+    with pytest.raises(YxError):
+        hip.attend(kv, 0, np.zeros((1, 4 * D), np.float32), 4)
+    hip.begin_pass(_meta([0], [16], [0], [1]))
+    k = np.ones((1, 2, D), np.float32)
+    hip.append(kv, 0, k, k * 2)
+    out = hip.attend(kv, 0, np.zeros((1, 4 * D), np.float32), 4)
+    assert np.all(out[0, :D] == 2.0)  # one key: the output is its value
