@@ -549,7 +549,9 @@ struct QkvIn {
 // its rows' q heads from qkv into LDS (write_rows' arithmetic, the same bits), and the
 // item of the group's last chunk normalises, rotates and stores the rows' key heads and
 // stores their value heads, before any wave reads a block.
-template <bool QKV>
+// UB: blocks per queue unit (4, or 2 for items of at most 32 blocks, so that every wave
+// has a unit).
+template <bool QKV, int UB>
 __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
     const AttnItem* __restrict__ items, const uint32_t* pos,
     const uint32_t* __restrict__ pages, const _Float16* kc, const _Float16* vc,
@@ -600,8 +602,8 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
     __syncthreads();
   }
 
-  const uint32_t nall = it.blk1 - it.blk0;  // at most 4 * kBalQuads (host-checked)
-  const uint32_t nq = (nall + 3) / 4;
+  const uint32_t nall = it.blk1 - it.blk0;  // at most UB * kBalQuads (host-checked)
+  const uint32_t nq = (nall + UB - 1) / UB;  // queue units
   const uint32_t bpp_mask = (1u << bpp_shift) - 1u;
   const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;
   const uint32_t* pt = pages + it.pt_off;
@@ -647,8 +649,8 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
   __asm__ volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
   uint32_t qc = static_cast<uint32_t>(wave);  // this wave's current quad
-  load_set(s0, 4 * qc);
-  load_set(s1, 4 * qc + 1);
+  load_set(s0, UB * qc);
+  load_set(s1, UB * qc + 1);
   half8 qb[4];
 #pragma unroll
   for (int pp = 0; pp < 4; ++pp) {
@@ -720,16 +722,15 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
     l = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = floatx4{0, 0, 0, 0};
-    // The quad's four blocks in turn; each load goes two blocks ahead, into the next
-    // quad for the last two.
-    process_set(s0, 4 * qc);
-    load_set(s0, 4 * qc + 2);
-    process_set(s1, 4 * qc + 1);
-    load_set(s1, 4 * qc + 3);
-    process_set(s0, 4 * qc + 2);
-    load_set(s0, 4 * qn);
-    process_set(s1, 4 * qc + 3);
-    load_set(s1, 4 * qn + 1);
+    // The unit's blocks in turn; each load goes two blocks ahead, into the next unit
+    // for the last two.
+    static_assert(UB == 2 || UB == 4, "units of two or four blocks");
+#pragma unroll
+    for (uint32_t j = 0; j < UB; ++j) {
+      BlockRegs& set = (j & 1) ? s1 : s0;
+      process_set(set, UB * qc + j);
+      load_set(set, j + 2 < UB ? UB * qc + j + 2 : UB * qn + (j + 2 - UB));
+    }
     // Join the hi and lo columns and store the quad's state in its slot.
 #pragma unroll
     for (int j = 0; j < 8; ++j)

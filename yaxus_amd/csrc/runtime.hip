@@ -111,7 +111,8 @@ struct AttnPlan {
   bool prefill = false;  // MFMA tiles over LDS (many rows per sequence) vs split-K decode
   std::vector<yx::PrefillItem> pitems;
   int nt = 1;
-  bool balanced = false;  // one tile, items of at most kBalQuads quads: waves share a queue
+  bool balanced = false;  // one tile, items of at most 4 * kBalQuads blocks: waves share a queue
+  bool small_units = false;  // balanced with items of at most 2 * kBalQuads blocks: 2-block units
   std::vector<yx::AttnItem> items;
   DevBuf d_items;
   bool fusable = false;  // the append can run inside the attention kernel
@@ -308,6 +309,10 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
                                   ? std::max<size_t>(1, static_cast<size_t>(c->target_waves) / waves)
                                   : static_cast<size_t>(c->cus);
   size_t cb = (work + target_items - 1) / target_items;
+  // At least a unit of blocks per wave (two blocks in the one-tile kernel, whose small
+  // items take 2-block units): with less, waves of every work item sit idle and the
+  // extra chunks only lengthen the merge (small passes, e.g. sliding windows).
+  if (c->target_waves == 0) cb = std::max<size_t>(cb, (nt == 1 ? 2 : 4) * waves);
   // Each wave's page ids fit its 64 lanes: at most 64 blocks per wave.
   cb = std::max<size_t>(1, std::min<size_t>({cb, static_cast<size_t>(c->max_chunk_blocks), 64 * waves}));
 
@@ -357,6 +362,9 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   plan.balanced = nt == 1 && c->decode_shape == 0;
   for (const yx::AttnItem& w : plan.items)
     if (w.blk1 - w.blk0 > 4 * yx::kBalQuads) plan.balanced = false;
+  plan.small_units = plan.balanced;
+  for (const yx::AttnItem& w : plan.items)
+    if (w.blk1 - w.blk0 > 2 * yx::kBalQuads) plan.small_units = false;
   plan.slots = slot;
   plan.counters = subs.size();
   if (plan.items.size() > 0x7fffffff) return fail(YX_ERR_UNSUPPORTED, "too many work items");
@@ -446,17 +454,16 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
                      static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],       \
                      po_bytes, pml_bytes, H, HK, P, W, scale_log2)
   if (plan->balanced) {
-    if (qkv)
-      hipLaunchKernelGGL(yx::paged_attn_decode_balanced<true>, grid, dim3(64 * yx::kBalWaves), 0,
-                         c->stream, items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml,
-                         cnt, nullptr, nullptr, static_cast<const uint32_t*>(c->d_slot.p),
-                         kv->k[layer], kv->v[layer], po_bytes, pml_bytes, H, HK, P, W, scale_log2,
-                         *qkv);
-    else
-      hipLaunchKernelGGL(yx::paged_attn_decode_balanced<false>, grid, dim3(64 * yx::kBalWaves), 0,
-                         c->stream, items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml,
-                         cnt, knew, vnew, static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer],
-                         kv->v[layer], po_bytes, pml_bytes, H, HK, P, W, scale_log2, yx::QkvIn{});
+#define YX_LAUNCH_BAL(QKV, UB, KN, VN, IN)                                                          \
+  hipLaunchKernelGGL((yx::paged_attn_decode_balanced<QKV, UB>), grid, dim3(64 * yx::kBalWaves), 0,  \
+                     c->stream, items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml,     \
+                     cnt, KN, VN, static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer],        \
+                     kv->v[layer], po_bytes, pml_bytes, H, HK, P, W, scale_log2, IN)
+    if (qkv && plan->small_units) YX_LAUNCH_BAL(true, 2, nullptr, nullptr, *qkv);
+    else if (qkv) YX_LAUNCH_BAL(true, 4, nullptr, nullptr, *qkv);
+    else if (plan->small_units) YX_LAUNCH_BAL(false, 2, knew, vnew, yx::QkvIn{});
+    else YX_LAUNCH_BAL(false, 4, knew, vnew, yx::QkvIn{});
+#undef YX_LAUNCH_BAL
   } else switch (plan->nt) {
     case 1: YX_LAUNCH_DECODE(1); break;
     case 2: YX_LAUNCH_DECODE(2); break;
