@@ -70,8 +70,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
   // A ring of stages; each holds SB blocks of K as [p][g][key] (4 KiB each) and then SB
   // blocks of V as [key][128] (4 KiB each).
   __shared__ half8 ring[kRing][2 * SB * 256];
-  const PrefillItem it = items[blockIdx.x];
-  const uint32_t kh = blockIdx.y;
+  // One dimension, KV head fastest: workgroups start in the host's longest-first item
+  // order across all KV heads.
+  const PrefillItem it = items[blockIdx.x / hkv];
+  const uint32_t kh = blockIdx.x % hkv;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int c = lane & 15, g = lane >> 4;

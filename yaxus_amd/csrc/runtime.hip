@@ -421,8 +421,8 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     while ((16u << shift) < kv->page) ++shift;
     hipEvent_t e0;
     if ((rc = prof_begin(c, YX_KERNEL_ATTENTION, &e0))) return rc;
-    hipLaunchKernelGGL(yx::paged_attn_prefill, dim3(static_cast<unsigned>(plan->pitems.size()),
-                       static_cast<unsigned>(hkv)), dim3(64 * yx::kPrefillWaves), 0, c->stream,
+    hipLaunchKernelGGL(yx::paged_attn_prefill, dim3(static_cast<unsigned>(plan->pitems.size() * hkv)),
+                       dim3(64 * yx::kPrefillWaves), 0, c->stream,
                        static_cast<const yx::PrefillItem*>(plan->d_items.p),
                        static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_pages.p),
                        kv->k[layer], kv->v[layer], q, out, static_cast<uint32_t>(hq),
