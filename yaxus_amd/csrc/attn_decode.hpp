@@ -589,7 +589,7 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
         const float* ks = qi_in.qkv + static_cast<size_t>(rr) * cols + qd + kh * kD;
         norm_rope_head(ks, qi_in.k_norm, qi_in.rope_cs, qi_in.rope_len, pos[rr], qi_in.eps, lane,
                        sh.qsq[wave], o0, o1);
-        store_kv_head(o0, o1, ks + kvd, kv_slot[rr], kh, hkv, 16u << bpp_shift, lane, kw, vw);
+        store_kv_head(o0, o1, ks + kvd, kv_slot[rr], kh, hkv, bpp_shift + 4, lane, kw, vw);
       }
     }
     // Stores complete, then the barrier orders them (and the queries in LDS) before

@@ -3,10 +3,9 @@
 // (crates/yaxus-backend-cpu/src/lib.rs:359-385), the step before attention, which the
 // reference GPU backend runs as QK_ROPE (crates/yaxus-backend-gpu/src/shaders.rs:285-341).
 //
-// One wave per (row, head) of the row's hq query heads and hkv key heads (the wave of a
-// key head also stores that head's value). Lane j holds dims j and j + 64, the pair
-// RoPE rotates together. The arithmetic is the CPU backend's, in its order, so the
-// results carry the same bits:
+// Lane j of a wave holds dims j and j + 64 of a head, the pair RoPE rotates together
+// (a key head's wave also stores that head's value). The arithmetic is the CPU
+// backend's, in its order, so the results carry the same bits:
 //   sum of squares: one lane adds the 128 squares in dim order (rmsnorm_row, lib.rs:296-302);
 //   r = 1 / sqrt(sum / 128 + eps) with correctly rounded division and square root;
 //   y = (1 + w) * (x * r);
@@ -23,8 +22,6 @@
 #include "kv_kernels.hpp"
 
 namespace yx {
-
-static constexpr int kRopeWaves = 4;
 
 // One wave, one head vector `src` (128 f32): RMSNorm with weights w (offset 1) and
 // half-split RoPE at position p; returns this lane's results for dims lane and
@@ -55,13 +52,14 @@ __device__ __forceinline__ void norm_rope_head(const float* __restrict__ src, co
 }
 
 // Stores one key head (k already normalised and rotated: lane's dims lane, lane + 64)
-// and its raw value head `vsrc` (128 f32) at `slot`: binary16, nearest even.
+// and its raw value head `vsrc` (128 f32) at `slot` (pages of 1 << page_shift slots):
+// binary16, nearest even.
 __device__ __forceinline__ void store_kv_head(float k0, float k1, const float* __restrict__ vsrc,
                                               uint32_t slot, uint32_t kh, uint32_t hkv,
-                                              uint32_t page_size, uint32_t lane, _Float16* kc,
+                                              uint32_t page_shift, uint32_t lane, _Float16* kc,
                                               _Float16* vc) {
-  const uint32_t off = slot % page_size;
-  const size_t region = (static_cast<size_t>(slot / page_size) * hkv + kh) * page_size * 128;
+  const uint32_t off = slot & ((1u << page_shift) - 1u);
+  const size_t region = ((static_cast<size_t>(slot >> page_shift) * hkv + kh) * 128) << page_shift;
   kc[region + k_offset(off, lane / 8) + lane % 8] = static_cast<_Float16>(k0);
   kc[region + k_offset(off, (lane + 64) / 8) + lane % 8] = static_cast<_Float16>(k1);
   if (lane < 16) {  // the value row: 16 lanes of 16 bytes
@@ -75,31 +73,118 @@ __device__ __forceinline__ void store_kv_head(float k0, float k1, const float* _
   }
 }
 
-__global__ __launch_bounds__(64 * kRopeWaves) void qk_norm_rope_append(
+// write_rows over a whole pass: the pass's head vectors (per row its hq query heads,
+// then its hkv key heads; vector i = row i / (hq + hkv)) in workgroups of kRopeVecs.
+// Each workgroup stages its vectors in LDS (coalesced: a row's q and k heads are
+// contiguous in qkv), then lanes of one wave add each vector's 128 squares serially in
+// dim order, one lane per vector (the CPU backend's order, so the same bits; a wave per
+// vector with one lane adding, as the decode kernel does for its few rows, leaves 63 of
+// 64 lanes idle), and then the four waves normalise, rotate and store, a lane per dim
+// pair (j, j + 64). Rows of 129 floats keep the serial reads free of bank conflicts.
+// Small workgroups keep many in flight: the per-workgroup chain of loads and the
+// serial sum, not the arithmetic, sets the time.
+static constexpr int kRopeVecs = 16;  // 16: 18.0 us at 4096 rows; 32: 19.1; 64: 24.6
+static constexpr int kRopeThreads = 256;
+
+__global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append(
     const float* __restrict__ qkv, const float* __restrict__ q_norm,
     const float* __restrict__ k_norm, const float* __restrict__ rope_cs, uint32_t rope_len,
     float eps, const uint32_t* __restrict__ pos, const uint32_t* __restrict__ kv_slot,
     _Float16* __restrict__ kc, _Float16* __restrict__ vc, float* __restrict__ q_out,
-    uint32_t hq, uint32_t hkv, uint32_t page_size) {
-  __shared__ float sq[kRopeWaves][128];
-  const uint32_t row = blockIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const uint32_t lane = threadIdx.x & 63;
-  const uint32_t h = blockIdx.y * kRopeWaves + wave;  // head: q heads, then key heads
-  if (h >= hq + hkv) return;                          // whole wave
-  const bool is_q = h < hq;
-  const uint32_t qd = hq * 128, kvd = hkv * 128;
-  const float* src = qkv + static_cast<size_t>(row) * (qd + 2 * kvd) + (is_q ? h * 128 : qd + (h - hq) * 128);
-  float o0, o1;
-  norm_rope_head(src, is_q ? q_norm : k_norm, rope_cs, rope_len, pos[row], eps, lane, sq[wave], o0, o1);
-  if (is_q) {
-    float* dst = q_out + static_cast<size_t>(row) * qd + h * 128;
-    dst[lane] = o0;
-    dst[lane + 64] = o1;
-    return;
+    uint32_t hq, uint32_t hkv, uint32_t page_shift, uint32_t nvec) {
+#pragma clang fp contract(off)
+  __shared__ float xs[kRopeVecs][129];
+  __shared__ float rs[kRopeVecs];
+  const uint32_t nh = hq + hkv, qd = hq * 128, kvd = hkv * 128, cols = qd + 2 * kvd;
+  const uint32_t v0 = blockIdx.x * kRopeVecs;
+  const uint32_t t = threadIdx.x, j = t & 63;
+  // Vector v0 + m is head (h0 + m) % nh of row row0 + (h0 + m) / nh; m < kRopeVecs.
+  const uint32_t row0 = v0 / nh, h0 = v0 - row0 * nh;
+  const float inv_nh = 1.0f / static_cast<float>(nh);
+  auto split = [&](uint32_t m, uint32_t& row, uint32_t& h) {
+    const uint32_t x = h0 + m;  // below kRopeVecs + nh: the float quotient is off by at most one
+    uint32_t d = static_cast<uint32_t>(static_cast<float>(x) * inv_nh);
+    if (d * nh > x) --d;
+    else if ((d + 1) * nh <= x) ++d;
+    row = row0 + d;
+    h = x - d * nh;
+  };
+  constexpr int kPer = kRopeVecs / (kRopeThreads / 64);  // vectors per thread in the last step
+  constexpr int kStage = kRopeVecs * 32 / kRopeThreads;    // float4 per thread when staging
+  // Loads in the order their results are needed, so that one chain (positions, then
+  // their cos/sin) overlaps the other (the vectors, then their sums): positions, the
+  // vectors, then cos/sin, slots and weights.
+  uint32_t prow[kPer], pslot[kPer];
+  float pcs[kPer], psn[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const uint32_t m = (t >> 6) + i * (kRopeThreads / 64);
+    uint32_t h;
+    split(m, prow[i], h);
+    if (v0 + m >= nvec) prow[i] = 0;
+    pslot[i] = pos[prow[i]];
   }
-  // The value head follows the key heads.
-  store_kv_head(o0, o1, src + kvd, kv_slot[row], h - hq, hkv, page_size, lane, kc, vc);
+  float4 stage[kStage];
+#pragma unroll
+  for (int k = 0; k < kStage; ++k) {
+    const uint32_t idx = k * kRopeThreads + t, v = idx / 32, c4 = idx % 32;
+    uint32_t row, h;
+    split(v, row, h);
+    if (v0 + v >= nvec) row = h = 0;
+    // The key heads follow the query heads in a row: vector h starts at h * 128.
+    stage[k] = *reinterpret_cast<const float4*>(qkv + static_cast<size_t>(row) * cols + h * 128 + c4 * 4);
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    pcs[i] = rope_cs[static_cast<size_t>(pslot[i]) * 64 + j];
+    psn[i] = rope_cs[(static_cast<size_t>(rope_len) + pslot[i]) * 64 + j];
+    pslot[i] = kv_slot[prow[i]];
+  }
+  const float qw0 = 1.0f + q_norm[j], qw1 = 1.0f + q_norm[j + 64];
+  const float kw0 = 1.0f + k_norm[j], kw1 = 1.0f + k_norm[j + 64];
+#pragma unroll
+  for (int k = 0; k < kStage; ++k) {
+    const uint32_t idx = k * kRopeThreads + t, v = idx / 32, c4 = idx % 32;
+    xs[v][c4 * 4] = stage[k].x;
+    xs[v][c4 * 4 + 1] = stage[k].y;
+    xs[v][c4 * 4 + 2] = stage[k].z;
+    xs[v][c4 * 4 + 3] = stage[k].w;
+  }
+  __syncthreads();
+  if (t < kRopeVecs) {  // one vector per lane of wave 0, its squares added in dim order
+    float ss = 0.0f;
+#pragma unroll
+    for (int i0 = 0; i0 < 128; i0 += 32) {
+      float x[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) x[i] = xs[t][i0 + i];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) ss += x[i] * x[i];
+    }
+    rs[t] = 1.0f / __builtin_sqrtf(ss / 128.0f + eps);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const uint32_t m = (t >> 6) + i * (kRopeThreads / 64), gv = v0 + m;
+    if (gv >= nvec) break;
+    uint32_t row, h;
+    split(m, row, h);
+    const bool is_q = h < hq;
+    const float r = rs[m];
+    const float y0 = (is_q ? qw0 : kw0) * (xs[m][j] * r);
+    const float y1 = (is_q ? qw1 : kw1) * (xs[m][j + 64] * r);
+    const float ab = y0 * pcs[i], bs = y1 * psn[i], bc = y1 * pcs[i], as = y0 * psn[i];
+    const float o0 = ab - bs, o1 = bc + as;
+    if (is_q) {
+      float* dst = q_out + static_cast<size_t>(row) * qd + h * 128;
+      dst[j] = o0;
+      dst[j + 64] = o1;
+    } else {
+      store_kv_head(o0, o1, qkv + static_cast<size_t>(row) * cols + qd + kvd + (h - hq) * 128,
+                    pslot[i], h - hq, hkv, page_shift, j, kc, vc);
+    }
+  }
 }
 
 }  // namespace yx

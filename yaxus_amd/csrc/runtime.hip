@@ -500,20 +500,23 @@ int check_qkv_rows(yx_ctx* c, size_t rope_len) {
   return YX_OK;
 }
 
-// write_rows on its own: one wave per (row, head).
+// write_rows on its own: workgroups of kRopeVecs head vectors.
 int qk_rope_impl(yx_ctx* c, yx_kv* kv, size_t layer, const yx::QkvIn& in, size_t hq, float* q_out) {
   if (c->rows == 0) return YX_OK;
   const size_t hkv = kv->hkv;
-  dim3 grid(static_cast<unsigned>(c->rows),
-            static_cast<unsigned>((hq + hkv + yx::kRopeWaves - 1) / yx::kRopeWaves));
+  const size_t nvec = c->rows * (hq + hkv);
+  if (nvec > 0xffffffffu) return fail(YX_ERR_UNSUPPORTED, "too many head vectors in the pass");
+  dim3 grid(static_cast<unsigned>((nvec + yx::kRopeVecs - 1) / yx::kRopeVecs));
+  uint32_t page_shift = 0;
+  while ((1u << page_shift) < kv->page) ++page_shift;
   hipEvent_t e0;
   int rc;
   if ((rc = prof_begin(c, YX_KERNEL_QK_ROPE, &e0))) return rc;
-  hipLaunchKernelGGL(yx::qk_norm_rope_append, grid, dim3(64 * yx::kRopeWaves), 0, c->stream, in.qkv,
+  hipLaunchKernelGGL(yx::qk_norm_rope_append, grid, dim3(yx::kRopeThreads), 0, c->stream, in.qkv,
                      in.q_norm, in.k_norm, in.rope_cs, in.rope_len, in.eps,
                      static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_slot.p),
                      kv->k[layer], kv->v[layer], q_out, static_cast<uint32_t>(hq),
-                     static_cast<uint32_t>(hkv), static_cast<uint32_t>(kv->page));
+                     static_cast<uint32_t>(hkv), page_shift, static_cast<uint32_t>(nvec));
   YX_HIP(hipGetLastError());
   return prof_end(c, YX_KERNEL_QK_ROPE, e0);
 }
