@@ -146,7 +146,10 @@ int yx_fill_normal(yx_ctx* ctx, void* dst, size_t n, int dtype, uint64_t seed, u
 
 /* HIP graph of the calls made between begin and end on the context's stream (each
  * must have run once before, so its work list is on the device); launch replays it.
- * The kernels leave their arrival counters at zero, so replays need no memset. */
+ * The kernels leave their arrival counters at zero, so replays need no memset. A new
+ * pass, an option, a destroyed arena or a grown scratch buffer since the capture makes
+ * launch fail with YX_ERR_INVALID (the graph would read memory that moved): capture
+ * again. Arenas and caller buffers the graph reads must stay allocated. */
 int yx_graph_begin(yx_ctx* ctx);
 int yx_graph_end(yx_ctx* ctx);
 int yx_graph_launch(yx_ctx* ctx);

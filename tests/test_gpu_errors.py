@@ -63,3 +63,31 @@ def test_the_context_still_works_after_an_error(hip, kv):
     hip.append(kv, 0, k, k * 2)
     out = hip.attend(kv, 0, np.zeros((1, 4 * D), np.float32), 4)
     assert np.all(out[0, :D] == 2.0)  # one key: the output is its value
+
+
+def test_a_graph_is_refused_after_the_pass_changes(hip, kv):
+    """A captured graph points at the pass's work list; a new pass frees it, so the graph
+    is refused instead of replayed."""
+    q = hip.tensor((1, 4 * D))
+    out = hip.tensor((1, 4 * D))
+    hip.begin_pass(_meta([5], [5], [0], [1]))
+    hip.attend(kv, 0, q, 4, out=out)
+    hip.graph_begin()
+    hip.attend(kv, 0, q, 4, out=out)
+    hip.graph_end()
+    hip.graph_launch()
+    hip.sync()
+    hip.set_option("attn_target_waves", 0)  # drops the work lists
+    with pytest.raises(YxError, match="capture it again"):
+        hip.graph_launch()
+    hip.attend(kv, 0, q, 4, out=out)
+    hip.graph_begin()
+    hip.attend(kv, 0, q, 4, out=out)
+    hip.graph_end()
+    hip.graph_launch()
+    hip.begin_pass(_meta([6], [6], [0], [1]))
+    with pytest.raises(YxError, match="capture it again"):
+        hip.graph_launch()
+    hip.sync()
+    for t in (q, out):
+        t.free()

@@ -38,8 +38,10 @@ int fail(int code, const std::string& m) {
 struct DevBuf {
   void* p = nullptr;
   size_t cap = 0;
+  uint64_t gen = 0;  // (re)allocations and releases so far: a captured graph's check
   int ensure(size_t bytes, hipStream_t s, bool zero = false) {
     if (bytes <= cap) return YX_OK;
+    ++gen;
     size_t n = std::max(bytes, cap * 2);
     n = (n + 255) & ~static_cast<size_t>(255);
     if (p) {
@@ -58,6 +60,7 @@ struct DevBuf {
   }
   void release() {
     if (p) (void)hipFree(p);
+    ++gen;
     p = nullptr;
     cap = 0;
   }
@@ -178,6 +181,18 @@ struct yx_ctx {
   bool capturing = false;
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
+  // What a captured graph's kernels point at: a new pass, an option, a destroyed arena
+  // (epoch) or a reallocated buffer (DevBuf::gen) invalidates it.
+  // Work lists are freed only with an epoch step; the other buffers count their own
+  // reallocations; both only grow, so the pair changes whenever either does.
+  uint64_t epoch = 0, graph_epoch = 0, graph_gens = 0;
+  uint64_t buffer_gens() const {
+    uint64_t s = 0;
+    for (const DevBuf* b : {&d_pos, &d_slot, &d_pages, &part_o, &part_ml, &counters, &io_a, &io_b,
+                            &io_c, &io_q})
+      s += b->gen;
+    return s;
+  }
 
   int set_device() {
     YX_HIP(hipSetDevice(device));
@@ -604,6 +619,7 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
     c->max_chunk_blocks = value;
   else
     return fail(YX_ERR_INVALID, std::string("unknown option ") + key);
+  ++c->epoch;
   for (auto& kv : c->plans) kv.second.d_items.release();
   c->plans.clear();
   return YX_OK;
@@ -661,6 +677,7 @@ int yx_kv_destroy(yx_ctx* c, yx_kv* kv) {
   if (c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
+    ++c->epoch;
   }
   for (auto* p : kv->k) (void)hipFree(p);
   for (auto* p : kv->v) (void)hipFree(p);
@@ -794,6 +811,7 @@ int yx_pass_begin(yx_ctx* c, size_t rows, const uint32_t* pos, const uint32_t* k
   int rc = c->set_device();
   if (rc) return rc;
   c->have_pass = false;
+  ++c->epoch;
   for (auto& kv : c->plans) kv.second.d_items.release();
   c->plans.clear();
   c->rows = rows;
@@ -1019,11 +1037,17 @@ int yx_graph_end(yx_ctx* c) {
   c->graph = g;
   c->graph_exec = nullptr;
   YX_HIP(hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0));
+  c->graph_epoch = c->epoch;
+  c->graph_gens = c->buffer_gens();
   return YX_OK;
 }
 
 int yx_graph_launch(yx_ctx* c) {
   if (!c || !c->graph_exec) return fail(YX_ERR_INVALID, "no captured graph");
+  if (c->epoch != c->graph_epoch || c->buffer_gens() != c->graph_gens)
+    return fail(YX_ERR_INVALID,
+                "the pass, an option, an arena or a buffer changed since the graph was captured; "
+                "capture it again");
   int rc = c->set_device();
   if (rc) return rc;
   YX_HIP(hipGraphLaunch(c->graph_exec, c->stream));
