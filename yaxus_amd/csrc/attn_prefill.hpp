@@ -3,20 +3,23 @@
 // The same arithmetic as `LayerPass::attend` (crates/yaxus-backend-cpu/src/lib.rs:
 // 389-427) for passes with many rows per sequence, the shape the reference's tiled
 // kernel serves (ATTN_TILE, crates/yaxus-backend-gpu/src/shaders.rs:422-592: 32 rows x
-// 32-key blocks, f32 SIMT). Here a workgroup of 4 waves takes a tile of consecutive
-// rows of one sequence and one KV head; its (row, query head) pairs are logical rows,
-// 32 per wave as 2 MFMA tiles of 16 columns. Keys stream through LDS in stages of 2
-// blocks of 16 (two buffers: stage s+1 is fetched from HBM into registers while stage s
-// is computed, then written to the other buffer), and every wave reads them there:
+// 32-key blocks, f32 SIMT). Here a workgroup of 8 waves (two per SIMD) takes a tile of
+// kPrefillRows logical rows, the (row, query head) pairs of consecutive rows of one
+// sequence and one KV head; each wave owns 16 of them, the 16 columns of its MFMA tile.
+// Keys stream from HBM straight into a 4-stage LDS ring of 64-key stages
+// (global_load_lds_dwordx4, no registers; three stages in flight while one is computed),
+// and every wave reads them there. Per 32 keys:
 //   S^T[key][row] = K . Q^T      8 x v_mfma_f32_16x16x32_f16 per tile (q as hi + lo f16)
-//   online softmax per column, once per 32 keys (permlane swaps across lane halves);
-//   the accumulator is rescaled only when a column's maximum moved
-//   O^T += V^T P^T               16 x v_mfma_f32_16x16x32_f16 per tile and 32 keys (P hi + lo)
+//   online softmax per column, once per 32 keys (permlane swaps across lane groups);
+//   the accumulator is rescaled only when a column's maximum grew by more than
+//   kLazyRescale
+//   O^T += V^T P^T               16 x v_mfma_f32_16x16x32_f16 per tile (P hi + lo)
 // q and P each go in as a binary16 hi part plus a lo part, two products into one
-// result, so both keep ~2^-22 relative accuracy (a single rounding costs up to 6e-4
-// absolute on few-key rows); K and V are binary16 already. This doubles the MFMA work
-// of the plain-f16 form. The tests compare with the f32 oracle and an f64 brute force.
-// Blocks no row of a wave can see (causal, window) are skipped by that wave.
+// result, so both keep ~2^-22 relative accuracy (a single rounding of P costs up to
+// 5e-4 absolute against the f32 oracle, 1.3e-3 with q three times larger); K and V are
+// binary16 already. This doubles the MFMA work of the plain-f16 form. The tests compare
+// with the f32 oracle and an f64 brute force. Key pairs no column of a wave can see
+// (causal, window) are skipped by that wave.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
