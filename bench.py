@@ -179,6 +179,31 @@ def _time_write_rows(hip, kv, pr, layers, steps):
     return us, rows * (cols * 4 + HQ * D * 4 + HKV * D * 2 * 2)
 
 
+def _time_attention_kernel(hip, kv, pr, layers, hq, steps):
+    """Average duration of the attention kernel alone (events around each launch of
+    the same fused append + attention calls, not graph-replayed): µs per launch."""
+    from yaxus_amd._lib import YX_KERNEL_ATTENTION
+
+    rows = len(pr.meta.pos)
+    q, out = hip.tensor((rows, hq * D)), hip.tensor((rows, hq * D))
+    k, v = hip.tensor((rows, HKV * D)), hip.tensor((rows, HKV * D))
+    for i, t in enumerate((q, k, v)):
+        hip.fill_normal(t.ptr, t.nbytes // 4, False, SEED + 99, i << 32)
+    hip.begin_pass(pr.meta)
+    for l in range(layers):
+        hip.attend_append(kv, l, k, v, q, hq, out=out)
+    hip.sync()
+    hip.profile(True)
+    for _ in range(steps):
+        for l in range(layers):
+            hip.attend_append(kv, l, k, v, q, hq, out=out)
+    hip.profile(False)
+    ms, n = hip.profile_read(YX_KERNEL_ATTENTION)
+    for t in (q, out, k, v):
+        t.free()
+    return ms * 1000.0 / max(n, 1)
+
+
 def _time_backend_attention(hip, kv, pr, layers, steps):
     """Backend::attention in full (write_rows then attend) per layer for the pass `pr`,
     device inputs: (us one launch, us as write_rows + attention launches)."""
@@ -218,94 +243,108 @@ def _time_backend_attention(hip, kv, pr, layers, steps):
     return res
 
 
-def bench_configs(hip, steps=10, include_long=True):
-    """BASELINE configurations 2-5 at full size (one JSON object per configuration)."""
+def bench_configs(hip, steps=10, include_long=True, only=None):
+    """BASELINE configurations 2-5 at full size (one JSON object per configuration);
+    `only`: a set of names among cfg2, cfg3, cfg4, cfg5 to run (all when None)."""
     from yaxus_amd import KvCache
     from yaxus_amd.data import uniform_ints
 
+    def want(name):
+        return only is None or name in only
+
     res = {}
-    # cfg2: 16 requests share a 1024-token prefix (64 refcounted pages); suffixes
-    # U[512, 3072]; one decode step over 24 layers.
-    pool, layers = 4096, 24
-    cache = KvCache(pool, 1 << 20, PAGE)
-    _scatter(cache, pool, SEED + 2)
-    base = cache.new_seq()
-    cache.append([(base, [1] * 1024)], [])
-    suf = uniform_ints(B, 512, 3072, SEED + 2)
-    seqs = [cache.fork(base, 1024, []) for _ in range(B)]
-    for s, n in zip(seqs, suf):
-        cache.append([(s, [1] * int(n))], [])
-    pr = cache.append([(s, [2]) for s in seqs], [])
-    kv = hip.new_kv(layers, pool, PAGE, HKV, D)
-    _fill_arena(hip, kv, layers, SEED + 2)
-    us = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, steps) / layers
-    ctx = [1024 + int(n) + 1 for n in suf]
-    logical = sum(ctx) * HKV * D * 2 * 2
-    unique = (1024 + int(sum(suf)) + B) * HKV * D * 2 * 2
-    wr_us, wr_bytes = _time_write_rows(hip, kv, pr, layers, steps)
-    ba_one, ba_two = _time_backend_attention(hip, kv, pr, layers, steps)
-    res["cfg2_prefix_decode"] = {"us_per_layer_step": round(us, 2),
-                                 "backend_attention_us_one_launch": round(ba_one, 2),
-                                 "backend_attention_us_two_launches": round(ba_two, 2),
-                                 "logical_GBs": round(logical / us / 1e3, 1),
-                                 "unique_GBs": round(unique / us / 1e3, 1),
-                                 "logical_bytes": logical, "unique_bytes": unique,
-                                 "write_rows_us_per_layer": round(wr_us, 2)}
-    kv.destroy()
-    # cfg3: 16 requests append a 256-token chunk on contexts U[0, 2048] that leave a
-    # half-filled tail page; causal within the chunk; 24 layers.
-    pool = 4096
-    cache = KvCache(pool, 1 << 20, PAGE)
-    _scatter(cache, pool, SEED + 3)
-    prior = [int(x) // 16 * 16 + 8 for x in uniform_ints(B, 0, 2040, SEED + 3)]
-    seqs = [cache.new_seq() for _ in range(B)]
-    for s, n in zip(seqs, prior):
-        cache.append([(s, [1] * n)], [])
-    pr = cache.append([(s, [2] * 256) for s in seqs], [])
-    kv = hip.new_kv(layers, pool, PAGE, HKV, D)
-    _fill_arena(hip, kv, layers, SEED + 3)
-    us = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, max(2, steps // 2)) / layers
-    flops = sum(4 * HQ * D * (256 * p + 256 * 257 // 2) for p in prior)
-    wr_us, wr_bytes = _time_write_rows(hip, kv, pr, layers, max(2, steps // 2))
-    res["cfg3_chunked_prefill"] = {"us_per_layer_step": round(us, 2),
-                                   "TFLOPs": round(flops / us / 1e6, 2),
-                                   "mfma_util_vs_2.5PF": round(flops / us / 1e6 / 2500.0, 4),
-                                   "flops_per_layer": flops,
-                                   "write_rows_us_per_layer": round(wr_us, 2),
-                                   "write_rows_GBs": round(wr_bytes / wr_us / 1e3, 1)}
-    kv.destroy()
-    # cfg5: 16 requests of ctx 4096 (2048 shared) verify 5 draft tokens (5 causal
-    # rows each); then 8 fork from a partly filled tail page (copy on write) and roll
-    # back a seeded count in [0, 5]; 24 layers.
-    pool = 8192
-    cache = KvCache(pool, 1 << 20, PAGE)
-    _scatter(cache, pool, SEED + 5)
-    base = cache.new_seq()
-    cache.append([(base, [1] * 2048)], [])
-    seqs = [cache.fork(base, 2048, []) for _ in range(B)]
-    for s in seqs:
-        cache.append([(s, [1] * (4096 - 2048 - 5))], [])
-    pr = cache.append([(s, [2] * 5) for s in seqs], [])
-    kv = hip.new_kv(layers, pool, PAGE, HKV, D)
-    _fill_arena(hip, kv, layers, SEED + 5)
-    us_verify = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, steps) / layers
-    t0 = time.perf_counter()
-    copies = []
-    forks = [cache.fork(s, cache.seq_len(s) - 3, copies) for s in seqs[:8]]
-    back = uniform_ints(len(seqs) + len(forks), 0, 5, SEED + 55)
-    for s, n in zip(seqs + forks, back):
-        cache.truncate(s, cache.seq_len(s) - int(n))
-    host_us = (time.perf_counter() - t0) * 1e6
-    hip.timer_start()
-    hip.copy_pages(kv, copies)
-    copy_us = hip.timer_stop() * 1000.0
-    bytes_verify = sum(4096 for _ in seqs) * HKV * D * 2 * 2
-    res["cfg5_verify_fork"] = {"us_per_layer_step_verify": round(us_verify, 2),
-                               "verify_logical_GBs": round(bytes_verify / us_verify / 1e3, 1),
-                               "fork_copies": len(copies), "copy_us_all_layers": round(copy_us, 2),
-                               "host_fork_rollback_us": round(host_us, 1)}
-    kv.destroy()
-    if include_long:
+    layers = 24
+    if want('cfg2'):
+        # cfg2: 16 requests share a 1024-token prefix (64 refcounted pages); suffixes
+        # U[512, 3072]; one decode step over 24 layers.
+        pool, layers = 4096, 24
+        cache = KvCache(pool, 1 << 20, PAGE)
+        _scatter(cache, pool, SEED + 2)
+        base = cache.new_seq()
+        cache.append([(base, [1] * 1024)], [])
+        suf = uniform_ints(B, 512, 3072, SEED + 2)
+        seqs = [cache.fork(base, 1024, []) for _ in range(B)]
+        for s, n in zip(seqs, suf):
+            cache.append([(s, [1] * int(n))], [])
+        pr = cache.append([(s, [2]) for s in seqs], [])
+        kv = hip.new_kv(layers, pool, PAGE, HKV, D)
+        _fill_arena(hip, kv, layers, SEED + 2)
+        us = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, steps) / layers
+        ctx = [1024 + int(n) + 1 for n in suf]
+        logical = sum(ctx) * HKV * D * 2 * 2
+        unique = (1024 + int(sum(suf)) + B) * HKV * D * 2 * 2
+        wr_us, wr_bytes = _time_write_rows(hip, kv, pr, layers, steps)
+        ba_one, ba_two = _time_backend_attention(hip, kv, pr, layers, steps)
+        res["cfg2_prefix_decode"] = {"us_per_layer_step": round(us, 2),
+                                     "backend_attention_us_one_launch": round(ba_one, 2),
+                                     "backend_attention_us_two_launches": round(ba_two, 2),
+                                     "logical_GBs": round(logical / us / 1e3, 1),
+                                     "unique_GBs": round(unique / us / 1e3, 1),
+                                     "logical_bytes": logical, "unique_bytes": unique,
+                                     "write_rows_us_per_layer": round(wr_us, 2)}
+        kv.destroy()
+    if want('cfg3'):
+        # cfg3: 16 requests append a 256-token chunk on contexts U[0, 2048] that leave a
+        # half-filled tail page; causal within the chunk; 24 layers.
+        pool = 4096
+        cache = KvCache(pool, 1 << 20, PAGE)
+        _scatter(cache, pool, SEED + 3)
+        prior = [int(x) // 16 * 16 + 8 for x in uniform_ints(B, 0, 2040, SEED + 3)]
+        seqs = [cache.new_seq() for _ in range(B)]
+        for s, n in zip(seqs, prior):
+            cache.append([(s, [1] * n)], [])
+        pr = cache.append([(s, [2] * 256) for s in seqs], [])
+        kv = hip.new_kv(layers, pool, PAGE, HKV, D)
+        _fill_arena(hip, kv, layers, SEED + 3)
+        us = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, max(2, steps // 2)) / layers
+        flops = sum(4 * HQ * D * (256 * p + 256 * 257 // 2) for p in prior)
+        wr_us, wr_bytes = _time_write_rows(hip, kv, pr, layers, max(2, steps // 2))
+        k_us = _time_attention_kernel(hip, kv, pr, layers, HQ, max(2, steps // 2))
+        # us_per_layer_step: the K/V append launch plus the prefill kernel, graph-replayed;
+        # attn_kernel_us: the prefill kernel alone (HIP events around each launch).
+        res["cfg3_chunked_prefill"] = {"us_per_layer_step": round(us, 2),
+                                       "TFLOPs": round(flops / us / 1e6, 2),
+                                       "mfma_util_vs_2.5PF": round(flops / us / 1e6 / 2500.0, 4),
+                                       "attn_kernel_us": round(k_us, 2),
+                                       "attn_kernel_TFLOPs": round(flops / k_us / 1e6, 2),
+                                       "attn_kernel_mfma_util_vs_2.5PF": round(flops / k_us / 1e6 / 2500.0, 4),
+                                       "flops_per_layer": flops,
+                                       "write_rows_us_per_layer": round(wr_us, 2),
+                                       "write_rows_GBs": round(wr_bytes / wr_us / 1e3, 1)}
+        kv.destroy()
+    if want('cfg5'):
+        # cfg5: 16 requests of ctx 4096 (2048 shared) verify 5 draft tokens (5 causal
+        # rows each); then 8 fork from a partly filled tail page (copy on write) and roll
+        # back a seeded count in [0, 5]; 24 layers.
+        pool = 8192
+        cache = KvCache(pool, 1 << 20, PAGE)
+        _scatter(cache, pool, SEED + 5)
+        base = cache.new_seq()
+        cache.append([(base, [1] * 2048)], [])
+        seqs = [cache.fork(base, 2048, []) for _ in range(B)]
+        for s in seqs:
+            cache.append([(s, [1] * (4096 - 2048 - 5))], [])
+        pr = cache.append([(s, [2] * 5) for s in seqs], [])
+        kv = hip.new_kv(layers, pool, PAGE, HKV, D)
+        _fill_arena(hip, kv, layers, SEED + 5)
+        us_verify = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, steps) / layers
+        t0 = time.perf_counter()
+        copies = []
+        forks = [cache.fork(s, cache.seq_len(s) - 3, copies) for s in seqs[:8]]
+        back = uniform_ints(len(seqs) + len(forks), 0, 5, SEED + 55)
+        for s, n in zip(seqs + forks, back):
+            cache.truncate(s, cache.seq_len(s) - int(n))
+        host_us = (time.perf_counter() - t0) * 1e6
+        hip.timer_start()
+        hip.copy_pages(kv, copies)
+        copy_us = hip.timer_stop() * 1000.0
+        bytes_verify = sum(4096 for _ in seqs) * HKV * D * 2 * 2
+        res["cfg5_verify_fork"] = {"us_per_layer_step_verify": round(us_verify, 2),
+                                   "verify_logical_GBs": round(bytes_verify / us_verify / 1e3, 1),
+                                   "fork_copies": len(copies), "copy_us_all_layers": round(copy_us, 2),
+                                   "host_fork_rollback_us": round(host_us, 1)}
+        kv.destroy()
+    if include_long and want('cfg4'):
         # cfg4: 4 requests of 32768 tokens over a 65536-page pool; 32 layers, 1 full
         # then 3 sliding (window 2048), repeated.
         pool, layers = 65536, 32
@@ -345,6 +384,8 @@ def main():
     ap.add_argument("--profile-run", action="store_true",
                     help="for rocprofv3: also run a 1 GiB device copy (the byte-counter "
                          "calibration point) and skip the CPU baseline")
+    ap.add_argument("--only", default=None,
+                    help="with --configs: comma-separated subset of cfg2,cfg3,cfg4,cfg5")
     ap.add_argument("--configs", action="store_true",
                     help="also measure BASELINE configurations 2-5 at full size (adds ~2 min)")
     ap.add_argument("--no-graph", action="store_true",
@@ -474,7 +515,7 @@ def main():
     }
     if args.configs:
         kv.destroy()
-        line["configs"] = bench_configs(hip)
+        line["configs"] = bench_configs(hip, only=set(args.only.split(",")) if args.only else None)
     print(json.dumps(line), flush=True)
     hip.close()
 
