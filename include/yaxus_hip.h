@@ -105,10 +105,12 @@ int yx_qk_rope_append_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* qkv
 
 /* Backend::attention in full (lib.rs:132; backend-cpu lib.rs:516-530: write_rows then
  * attend), device pointers, arguments as yx_qk_rope_append_dev and yx_attention_dev.
- * One launch when the pass is a one-tile decode pass (each group's rows in one work
- * item chain): the attention kernel normalises and rotates its rows' q heads into LDS
- * and the group's last work item stores the rows' K/V, with write_rows' bits; otherwise
- * write_rows runs as its own launch first. out `[rows][hq * 128]` f32. */
+ * A one-tile decode pass (each group's rows in one work item chain) takes one launch:
+ * the attention kernel normalises and rotates its rows' q heads into LDS and the
+ * group's last work item stores the rows' K/V. A prefill pass takes two: write_rows for
+ * the key and value heads, then the prefill kernel, which normalises and rotates its q
+ * heads itself. Other passes run write_rows, then attention. Every path has write_rows'
+ * bits. out `[rows][hq * 128]` f32. */
 int yx_attention_qkv_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* qkv,
                          const float* q_norm, const float* k_norm, const float* rope_cs,
                          size_t rope_len, float eps, float* out, size_t hq, size_t hkv,

@@ -301,11 +301,13 @@ def test_model_attention_two_passes_across_pages(hip, window):
 
 @pytest.mark.parametrize("hq,hkv,lens,k", [
     (16, 4, [1, 300, 17, 1000, 64], 1), (8, 2, [40, 513], 1), (16, 4, [40, 513, 7], 5),
-    (32, 2, [100, 2000], 1)])
+    (32, 2, [100, 2000], 1), (16, 4, [40, 513, 7], 40), (8, 8, [0, 130], 70)])
 def test_attention_in_one_launch_equals_two(hip, hq, hkv, lens, k):
-    """Backend::attention in full: the decode kernel that runs write_rows itself gives the
-    same bits (attention output and stored K/V) as write_rows then attention in two
-    launches, and both match the oracle. Verify passes (k > 1) take the two-launch path."""
+    """Backend::attention in full gives the same bits (attention output and stored K/V)
+    as write_rows then attention as separate calls, and both match the oracle: decode
+    passes in one launch (the decode kernel runs write_rows itself), verify passes (k = 5)
+    as write_rows then attention, prefill passes (k >= 32) as the key heads' write_rows
+    then the prefill kernel, which normalises and rotates its q heads itself."""
     from yaxus_amd.rope import inv_freq, rope_table
 
     f = inv_freq(D, 10000.0)
@@ -314,7 +316,7 @@ def test_attention_in_one_launch_equals_two(hip, hq, hkv, lens, k):
     for one_launch in (True, False):
         sc = Scenario(hip, pages=400, page=16, hkv=hkv, pool_seed=21)
         seqs = [sc.cache.new_seq() for _ in lens]
-        sc.prefill(dict(zip(seqs, lens)))
+        sc.prefill({s: n for s, n in zip(seqs, lens) if n})
         pr = sc.run_pass([(s, k) for s in seqs])
         rows = len(pr.meta.pos)
         qkv = sc.draw(rows * (hq + 2 * hkv) * D).reshape(rows, -1)
@@ -336,7 +338,7 @@ def test_attention_in_one_launch_equals_two(hip, hq, hkv, lens, k):
     rows = len(pr.meta.pos)
     sc = Scenario(hip, pages=400, page=16, hkv=hkv, pool_seed=21)
     seqs = [sc.cache.new_seq() for _ in lens]
-    sc.prefill(dict(zip(seqs, lens)))
+    sc.prefill({s: n for s, n in zip(seqs, lens) if n})
     pr = sc.run_pass([(s, k) for s in seqs])
     qkv = sc.draw(rows * (hq + 2 * hkv) * D).reshape(rows, -1)
     qn, kn = sc.draw(D) * 0.1, sc.draw(D) * 0.1

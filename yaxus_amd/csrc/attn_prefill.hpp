@@ -64,11 +64,16 @@ __device__ __forceinline__ void load_to_lds16(const void* src, uint32_t lds) {
 
 // Two waves per SIMD (at most 256 registers each), so one wave's softmax arithmetic
 // overlaps the other's matrix products.
+// QKV: q is not given; the kernel reads its rows' raw q heads from qkv and normalises
+// and rotates them itself, with write_rows' arithmetic (the same bits as
+// qk_norm_rope_append), the key heads having been stored before the launch.
+template <bool QKV>
 __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_attn_prefill(
     const PrefillItem* __restrict__ items, const uint32_t* pos,
     const uint32_t* __restrict__ pages, const _Float16* __restrict__ kc,
     const _Float16* __restrict__ vc, const float* q, float* __restrict__ out,
-    uint32_t hq, uint32_t hkv, uint32_t bpp_shift, uint32_t window, float scale_log2) {
+    uint32_t hq, uint32_t hkv, uint32_t bpp_shift, uint32_t window, float scale_log2,
+    QkvIn qi_in) {
   constexpr int NT = kPrefillTiles, SB = kStageBlocks;
   // A ring of stages; each holds SB blocks of K as [p][g][key] (4 KiB each) and then SB
   // blocks of V as [key][128] (4 KiB each).
@@ -117,6 +122,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
   // compiler cannot sink these loads below the stage loads.
   float4 qraw[NT][8];
   int rpos[NT], rlo[NT];
+  uint32_t rowp[NT];  // the column's position (row 0's for an empty column)
   bool has[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -127,7 +133,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
     const int p = static_cast<int>(pos[rr]);
     rpos[t] = has[t] ? p : -1;
     rlo[t] = (window > 0 && p + 1 > static_cast<int>(window)) ? p + 1 - static_cast<int>(window) : 0;
-    const float* qp = q + (static_cast<size_t>(rr) * hq + h) * kD + g * 8;
+    rowp[t] = p;
+    const float* qp = QKV ? qi_in.qkv + static_cast<size_t>(rr) * (hq + 2 * hkv) * kD + h * kD + g * 8
+                          : q + (static_cast<size_t>(rr) * hq + h) * kD + g * 8;
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
       qraw[t][2 * pp] = *reinterpret_cast<const float4*>(qp + pp * 32);
@@ -140,6 +148,58 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
 #pragma unroll
   for (int j = 0; j < kRing - 1; ++j) issue(j, j);
 
+  if constexpr (QKV) {
+    // write_rows for the columns' q heads. Lane g of a column holds dims
+    // 32 pp + 8 g + e; the sum of squares runs over dims 0..127 in order, so it passes
+    // from lane group to lane group every 8 dims (the owner adds, all take its sum).
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float x[32];
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const float4 a = qraw[t][2 * pp], b = qraw[t][2 * pp + 1];
+        x[8 * pp] = a.x; x[8 * pp + 1] = a.y; x[8 * pp + 2] = a.z; x[8 * pp + 3] = a.w;
+        x[8 * pp + 4] = b.x; x[8 * pp + 5] = b.y; x[8 * pp + 6] = b.z; x[8 * pp + 7] = b.w;
+      }
+      float ss = 0.0f;
+#pragma unroll
+      for (int s8 = 0; s8 < 16; ++s8) {
+        const int pp = s8 >> 2, owner = s8 & 3;
+        float cand = ss;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cand = cand + x[8 * pp + e] * x[8 * pp + e];
+        ss = __shfl(cand, c + 16 * owner);
+      }
+      const float r = 1.0f / __builtin_sqrtf(ss / 128.0f + qi_in.eps);
+      float y[32];
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int d = 32 * pp + 8 * g + e;
+          y[8 * pp + e] = (1.0f + qi_in.q_norm[d]) * (x[8 * pp + e] * r);
+        }
+      const float* cs_row = qi_in.rope_cs + static_cast<size_t>(rowp[t]) * 64;
+      const float* sn_row = qi_in.rope_cs + (static_cast<size_t>(qi_in.rope_len) + rowp[t]) * 64;
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int j = 32 * pp + 8 * g + e;  // dims j and j + 64 rotate together
+          const float y0 = y[8 * pp + e], y1 = y[8 * (pp + 2) + e];
+          const float cs = cs_row[j], sn = sn_row[j];
+          const float ab = y0 * cs, bs = y1 * sn, bc = y1 * cs, as = y0 * sn;
+          y[8 * pp + e] = ab - bs;
+          y[8 * (pp + 2) + e] = bc + as;
+        }
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        qraw[t][2 * pp] = float4{y[8 * pp], y[8 * pp + 1], y[8 * pp + 2], y[8 * pp + 3]};
+        qraw[t][2 * pp + 1] = float4{y[8 * pp + 4], y[8 * pp + 5], y[8 * pp + 6], y[8 * pp + 7]};
+      }
+    }
+  }
   half8 qh[NT][4], ql[NT][4];  // q as binary16 hi + lo parts
 #pragma unroll
   for (int t = 0; t < NT; ++t)

@@ -74,7 +74,8 @@ __device__ __forceinline__ void store_kv_head(float k0, float k1, const float* _
 }
 
 // write_rows over a whole pass: the pass's head vectors (per row its hq query heads,
-// then its hkv key heads; vector i = row i / (hq + hkv)) in workgroups of kRopeVecs.
+// then its hkv key heads, or the key heads only; vector i = row i / heads) in
+// workgroups of kRopeVecs.
 // Each workgroup stages its vectors in LDS (coalesced: a row's q and k heads are
 // contiguous in qkv), then lanes of one wave add each vector's 128 squares serially in
 // dim order, one lane per vector (the CPU backend's order, so the same bits; a wave per
@@ -91,11 +92,13 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append(
     const float* __restrict__ k_norm, const float* __restrict__ rope_cs, uint32_t rope_len,
     float eps, const uint32_t* __restrict__ pos, const uint32_t* __restrict__ kv_slot,
     _Float16* __restrict__ kc, _Float16* __restrict__ vc, float* __restrict__ q_out,
-    uint32_t hq, uint32_t hkv, uint32_t page_shift, uint32_t nvec) {
+    uint32_t hq, uint32_t hkv, uint32_t page_shift, uint32_t nvec, uint32_t first) {
 #pragma clang fp contract(off)
   __shared__ float xs[kRopeVecs][129];
   __shared__ float rs[kRopeVecs];
-  const uint32_t nh = hq + hkv, qd = hq * 128, kvd = hkv * 128, cols = qd + 2 * kvd;
+  // first = 0: every head; first = hq: the key heads only (the caller normalises the
+  // query heads itself). nh heads per row from head `first` on.
+  const uint32_t nh = hq + hkv - first, qd = hq * 128, kvd = hkv * 128, cols = qd + 2 * kvd;
   const uint32_t v0 = blockIdx.x * kRopeVecs;
   const uint32_t t = threadIdx.x, j = t & 63;
   // Vector v0 + m is head (h0 + m) % nh of row row0 + (h0 + m) / nh; m < kRopeVecs.
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append(
     if (d * nh > x) --d;
     else if ((d + 1) * nh <= x) ++d;
     row = row0 + d;
-    h = x - d * nh;
+    h = first + x - d * nh;
   };
   constexpr int kPer = kRopeVecs / (kRopeThreads / 64);  // vectors per thread in the last step
   constexpr int kStage = kRopeVecs * 32 / kRopeThreads;    // float4 per thread when staging

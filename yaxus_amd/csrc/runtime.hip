@@ -396,7 +396,8 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
 
 int append_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v);
 
-int qk_rope_impl(yx_ctx* c, yx_kv* kv, size_t layer, const yx::QkvIn& in, size_t hq, float* q_out);
+int qk_rope_impl(yx_ctx* c, yx_kv* kv, size_t layer, const yx::QkvIn& in, size_t hq, float* q_out,
+                 bool kv_only = false);
 
 // Attention of the pass's rows; with knew/vnew, the rows' K/V are stored first (in
 // the same kernel when the plan allows it, else by the append kernel before it); with
@@ -425,7 +426,10 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     if ((rc = append_impl(c, kv, layer, knew, vnew))) return rc;
     knew = vnew = nullptr;
   }
-  if (qkv && !(plan->balanced && plan->fusable)) {
+  if (qkv && plan->prefill) {
+    // The prefill kernel normalises and rotates its rows' q heads itself; K/V first.
+    if ((rc = qk_rope_impl(c, kv, layer, *qkv, hq, nullptr, true))) return rc;
+  } else if (qkv && !(plan->balanced && plan->fusable)) {
     if ((rc = c->io_q.ensure(std::max<size_t>(16, c->rows * hq * 128 * 4), c->stream))) return rc;
     if ((rc = qk_rope_impl(c, kv, layer, *qkv, hq, static_cast<float*>(c->io_q.p)))) return rc;
     q = static_cast<const float*>(c->io_q.p);
@@ -436,13 +440,21 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     while ((16u << shift) < kv->page) ++shift;
     hipEvent_t e0;
     if ((rc = prof_begin(c, YX_KERNEL_ATTENTION, &e0))) return rc;
-    hipLaunchKernelGGL(yx::paged_attn_prefill, dim3(static_cast<unsigned>(plan->pitems.size() * hkv)),
-                       dim3(64 * yx::kPrefillWaves), 0, c->stream,
+    const dim3 pgrid(static_cast<unsigned>(plan->pitems.size() * hkv));
+    if (qkv)
+      hipLaunchKernelGGL((yx::paged_attn_prefill<true>), pgrid, dim3(64 * yx::kPrefillWaves), 0, c->stream,
                        static_cast<const yx::PrefillItem*>(plan->d_items.p),
                        static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_pages.p),
                        kv->k[layer], kv->v[layer], q, out, static_cast<uint32_t>(hq),
                        static_cast<uint32_t>(hkv), shift, static_cast<uint32_t>(window),
-                       scale * yx::kLog2e);
+                       scale * yx::kLog2e, *qkv);
+    else
+      hipLaunchKernelGGL((yx::paged_attn_prefill<false>), pgrid, dim3(64 * yx::kPrefillWaves), 0, c->stream,
+                       static_cast<const yx::PrefillItem*>(plan->d_items.p),
+                       static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_pages.p),
+                       kv->k[layer], kv->v[layer], q, out, static_cast<uint32_t>(hq),
+                       static_cast<uint32_t>(hkv), shift, static_cast<uint32_t>(window),
+                       scale * yx::kLog2e, yx::QkvIn{});
     YX_HIP(hipGetLastError());
     return prof_end(c, YX_KERNEL_ATTENTION, e0);
   }
@@ -515,11 +527,13 @@ int check_qkv_rows(yx_ctx* c, size_t rope_len) {
   return YX_OK;
 }
 
-// write_rows on its own: workgroups of kRopeVecs head vectors.
-int qk_rope_impl(yx_ctx* c, yx_kv* kv, size_t layer, const yx::QkvIn& in, size_t hq, float* q_out) {
+// write_rows on its own: workgroups of kRopeVecs head vectors; with kv_only, the key
+// and value heads only (q_out unused).
+int qk_rope_impl(yx_ctx* c, yx_kv* kv, size_t layer, const yx::QkvIn& in, size_t hq, float* q_out,
+                 bool kv_only) {
   if (c->rows == 0) return YX_OK;
   const size_t hkv = kv->hkv;
-  const size_t nvec = c->rows * (hq + hkv);
+  const size_t nvec = c->rows * (kv_only ? hkv : hq + hkv);
   if (nvec > 0xffffffffu) return fail(YX_ERR_UNSUPPORTED, "too many head vectors in the pass");
   dim3 grid(static_cast<unsigned>((nvec + yx::kRopeVecs - 1) / yx::kRopeVecs));
   uint32_t page_shift = 0;
@@ -531,7 +545,8 @@ int qk_rope_impl(yx_ctx* c, yx_kv* kv, size_t layer, const yx::QkvIn& in, size_t
                      in.q_norm, in.k_norm, in.rope_cs, in.rope_len, in.eps,
                      static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_slot.p),
                      kv->k[layer], kv->v[layer], q_out, static_cast<uint32_t>(hq),
-                     static_cast<uint32_t>(hkv), page_shift, static_cast<uint32_t>(nvec));
+                     static_cast<uint32_t>(hkv), page_shift, static_cast<uint32_t>(nvec),
+                     static_cast<uint32_t>(kv_only ? hq : 0));
   YX_HIP(hipGetLastError());
   return prof_end(c, YX_KERNEL_QK_ROPE, e0);
 }
