@@ -243,6 +243,69 @@ def _time_backend_attention(hip, kv, pr, layers, steps):
     return res
 
 
+def cfg2_pass(KvCache):
+    """cfg2: 16 requests share a 1024-token prefix (64 refcounted pages); suffixes
+    U[512, 3072]; the decode pass appending one token to each. (cache, pass, pool,
+    suffix lengths)."""
+    from yaxus_amd.data import uniform_ints
+
+    pool = 4096
+    cache = KvCache(pool, 1 << 20, PAGE)
+    _scatter(cache, pool, SEED + 2)
+    base = cache.new_seq()
+    cache.append([(base, [1] * 1024)], [])
+    suf = uniform_ints(B, 512, 3072, SEED + 2)
+    seqs = [cache.fork(base, 1024, []) for _ in range(B)]
+    for s, n in zip(seqs, suf):
+        cache.append([(s, [1] * int(n))], [])
+    pr = cache.append([(s, [2]) for s in seqs], [])
+    return cache, pr, pool, suf
+
+
+def cfg3_pass(KvCache):
+    """cfg3: 16 requests append a 256-token chunk on contexts U[0, 2048] that leave a
+    half-filled tail page (causal within the chunk). (cache, pass, pool, prior lengths)."""
+    from yaxus_amd.data import uniform_ints
+
+    pool = 4096
+    cache = KvCache(pool, 1 << 20, PAGE)
+    _scatter(cache, pool, SEED + 3)
+    prior = [int(x) // 16 * 16 + 8 for x in uniform_ints(B, 0, 2040, SEED + 3)]
+    seqs = [cache.new_seq() for _ in range(B)]
+    for s, n in zip(seqs, prior):
+        cache.append([(s, [1] * n)], [])
+    pr = cache.append([(s, [2] * 256) for s in seqs], [])
+    return cache, pr, pool, prior
+
+
+def cfg4_pass(KvCache):
+    """cfg4: 4 requests of 32768 tokens over a 65536-page pool, one decode step.
+    (cache, pass, pool)."""
+    pool = 65536
+    cache = KvCache(pool, 1 << 20, PAGE)
+    _scatter(cache, pool, SEED + 4)
+    seqs = [cache.new_seq() for _ in range(4)]
+    for s in seqs:
+        cache.append([(s, [1] * 32767)], [])
+    pr = cache.append([(s, [2]) for s in seqs], [])
+    return cache, pr, pool
+
+
+def cfg5_pass(KvCache):
+    """cfg5: 16 requests of ctx 4096 (2048 shared) verifying 5 draft tokens (5 causal
+    rows each). (cache, pass, pool, sequences)."""
+    pool = 8192
+    cache = KvCache(pool, 1 << 20, PAGE)
+    _scatter(cache, pool, SEED + 5)
+    base = cache.new_seq()
+    cache.append([(base, [1] * 2048)], [])
+    seqs = [cache.fork(base, 2048, []) for _ in range(B)]
+    for s in seqs:
+        cache.append([(s, [1] * (4096 - 2048 - 5))], [])
+    pr = cache.append([(s, [2] * 5) for s in seqs], [])
+    return cache, pr, pool, seqs
+
+
 def bench_configs(hip, steps=10, include_long=True, only=None):
     """BASELINE configurations 2-5 at full size (one JSON object per configuration);
     `only`: a set of names among cfg2, cfg3, cfg4, cfg5 to run (all when None)."""
@@ -255,18 +318,9 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
     res = {}
     layers = 24
     if want('cfg2'):
-        # cfg2: 16 requests share a 1024-token prefix (64 refcounted pages); suffixes
-        # U[512, 3072]; one decode step over 24 layers.
-        pool, layers = 4096, 24
-        cache = KvCache(pool, 1 << 20, PAGE)
-        _scatter(cache, pool, SEED + 2)
-        base = cache.new_seq()
-        cache.append([(base, [1] * 1024)], [])
-        suf = uniform_ints(B, 512, 3072, SEED + 2)
-        seqs = [cache.fork(base, 1024, []) for _ in range(B)]
-        for s, n in zip(seqs, suf):
-            cache.append([(s, [1] * int(n))], [])
-        pr = cache.append([(s, [2]) for s in seqs], [])
+        # cfg2: one decode step over 24 layers.
+        cache, pr, pool, suf = cfg2_pass(KvCache)
+        layers = 24
         kv = hip.new_kv(layers, pool, PAGE, HKV, D)
         _fill_arena(hip, kv, layers, SEED + 2)
         us = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, steps) / layers
@@ -284,16 +338,8 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
                                      "write_rows_us_per_layer": round(wr_us, 2)}
         kv.destroy()
     if want('cfg3'):
-        # cfg3: 16 requests append a 256-token chunk on contexts U[0, 2048] that leave a
-        # half-filled tail page; causal within the chunk; 24 layers.
-        pool = 4096
-        cache = KvCache(pool, 1 << 20, PAGE)
-        _scatter(cache, pool, SEED + 3)
-        prior = [int(x) // 16 * 16 + 8 for x in uniform_ints(B, 0, 2040, SEED + 3)]
-        seqs = [cache.new_seq() for _ in range(B)]
-        for s, n in zip(seqs, prior):
-            cache.append([(s, [1] * n)], [])
-        pr = cache.append([(s, [2] * 256) for s in seqs], [])
+        # cfg3: the 256-row chunks over 24 layers.
+        cache, pr, pool, prior = cfg3_pass(KvCache)
         kv = hip.new_kv(layers, pool, PAGE, HKV, D)
         _fill_arena(hip, kv, layers, SEED + 3)
         us = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, max(2, steps // 2)) / layers
@@ -313,18 +359,9 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
                                        "write_rows_GBs": round(wr_bytes / wr_us / 1e3, 1)}
         kv.destroy()
     if want('cfg5'):
-        # cfg5: 16 requests of ctx 4096 (2048 shared) verify 5 draft tokens (5 causal
-        # rows each); then 8 fork from a partly filled tail page (copy on write) and roll
-        # back a seeded count in [0, 5]; 24 layers.
-        pool = 8192
-        cache = KvCache(pool, 1 << 20, PAGE)
-        _scatter(cache, pool, SEED + 5)
-        base = cache.new_seq()
-        cache.append([(base, [1] * 2048)], [])
-        seqs = [cache.fork(base, 2048, []) for _ in range(B)]
-        for s in seqs:
-            cache.append([(s, [1] * (4096 - 2048 - 5))], [])
-        pr = cache.append([(s, [2] * 5) for s in seqs], [])
+        # cfg5: the verify pass over 24 layers; then 8 requests fork from a partly
+        # filled tail page (copy on write) and roll back a seeded count in [0, 5].
+        cache, pr, pool, seqs = cfg5_pass(KvCache)
         kv = hip.new_kv(layers, pool, PAGE, HKV, D)
         _fill_arena(hip, kv, layers, SEED + 5)
         us_verify = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, steps) / layers
@@ -345,15 +382,9 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
                                    "host_fork_rollback_us": round(host_us, 1)}
         kv.destroy()
     if include_long and want('cfg4'):
-        # cfg4: 4 requests of 32768 tokens over a 65536-page pool; 32 layers, 1 full
-        # then 3 sliding (window 2048), repeated.
-        pool, layers = 65536, 32
-        cache = KvCache(pool, 1 << 20, PAGE)
-        _scatter(cache, pool, SEED + 4)
-        seqs = [cache.new_seq() for _ in range(4)]
-        for s in seqs:
-            cache.append([(s, [1] * 32767)], [])
-        pr = cache.append([(s, [2]) for s in seqs], [])
+        # cfg4: 32 layers, 1 full then 3 sliding (window 2048), repeated.
+        cache, pr, pool = cfg4_pass(KvCache)
+        layers = 32
         kv = hip.new_kv(layers, pool, PAGE, HKV, D)
         _fill_arena(hip, kv, layers, SEED + 4)
         windows = [0 if l % 4 == 0 else 2048 for l in range(layers)]
