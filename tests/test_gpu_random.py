@@ -1,7 +1,7 @@
 """Seeded random passes through the fused append + attention against the oracle: head
-shapes, page sizes, sequence counts, context lengths, rows per sequence (decode, verify
-and prefill rows mixed in one pass) and windows drawn per case. Each case also checks
-the appended K/V bits of every page the pass wrote."""
+shapes, page sizes (16-512), sequence counts, context lengths, rows per sequence
+(decode, verify and prefill rows mixed in one pass) and windows drawn per case. Each
+case also checks the appended K/V bits of every page the pass wrote."""
 
 import numpy as np
 import pytest
@@ -11,7 +11,7 @@ from tests.scenario import D, Scenario, close
 pytestmark = pytest.mark.gpu
 
 HEADS = [(16, 4), (8, 8), (32, 2), (16, 1), (8, 2), (4, 4)]
-PAGES = [16, 32, 64, 128]
+PAGES = [16, 32, 64, 128, 256, 512]
 ROWS = [1, 1, 1, 2, 5, 40]
 
 
