@@ -91,3 +91,25 @@ def test_a_graph_is_refused_after_the_pass_changes(hip, kv):
     hip.sync()
     for t in (q, out):
         t.free()
+
+
+def test_rejects_null_device_buffers(hip, kv):
+    """Null q, out, k or v on the device-pointer entry points is refused on the host
+    (a kernel given a null buffer would fault the GPU instead)."""
+    from yaxus_amd._lib import YX_OK
+
+    hip.begin_pass(_meta([5], [5], [0], [1]))
+    out = hip.tensor((1, 4 * D))
+    q = hip.tensor((1, 4 * D))
+    kk = hip.tensor((1, 2 * D))
+    scale = 1.0 / np.sqrt(D)
+    L = hip.L
+    assert L.yx_attention_dev(hip.ctx, kv.h, 0, None, out.ptr, 4, 2, 0, scale) != YX_OK
+    assert L.yx_attention_dev(hip.ctx, kv.h, 0, q.ptr, None, 4, 2, 0, scale) != YX_OK
+    assert L.yx_attention_append_dev(hip.ctx, kv.h, 0, kk.ptr, None, q.ptr, out.ptr, 4, 2, 0,
+                                     scale) != YX_OK
+    assert L.yx_kv_append_dev(hip.ctx, kv.h, 0, None, kk.ptr) != YX_OK
+    hip.attend(kv, 0, q, 4, out=out)  # the context still works
+    hip.sync()
+    for t in (out, q, kk):
+        t.free()

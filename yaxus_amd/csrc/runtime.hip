@@ -411,6 +411,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   if (hkv != kv->hkv) return fail(YX_ERR_INVALID, "hkv differs from the arena's");
   if (hq == 0 || hq % hkv != 0) return fail(YX_ERR_INVALID, "hq must be a positive multiple of hkv");
   if (c->rows == 0) return YX_OK;
+  if (!out || (!q && !qkv)) return fail(YX_ERR_INVALID, "null q or out");
   AttnPlan* plan;
   if (c->capturing && !c->plans.count(std::make_tuple(window, hq, hkv)))
     return fail(YX_ERR_INVALID, "run the call once before capturing it (its work list is uploaded then)");
@@ -506,6 +507,7 @@ int append_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float*
   int rc = check_kv(c, kv, layer);
   if (rc) return rc;
   if (c->rows == 0) return YX_OK;
+  if (!k || !v) return fail(YX_ERR_INVALID, "null k or v");
   const size_t threads = c->rows * kv->hkv * 16;
   dim3 grid(static_cast<unsigned>((threads + 255) / 256), 2);
   hipEvent_t e0;
@@ -648,7 +650,7 @@ int yx_kv_create(yx_ctx* c, size_t layers, size_t pages, size_t page_size, size_
   if (page_size < 16 || (page_size & (page_size - 1)) != 0)
     return fail(YX_ERR_UNSUPPORTED, "page size must be a power of two, at least 16");
   if (layers == 0 || pages == 0 || hkv == 0) return fail(YX_ERR_INVALID, "empty arena");
-  if (pages * page_size > 0xffffffffull) return fail(YX_ERR_INVALID, "arena slots are 32-bit");
+  if (pages > 0xffffffffull / page_size) return fail(YX_ERR_INVALID, "arena slots are 32-bit");
   int rc = c->set_device();
   if (rc) return rc;
   auto* kv = new yx_kv();
@@ -752,6 +754,7 @@ int yx_kv_copy_pages(yx_ctx* c, yx_kv* kv, const uint32_t* src, const uint32_t* 
 static int page_io(yx_ctx* c, yx_kv* kv, size_t layer, const uint32_t* pages, size_t n, void* k,
                    void* v, bool read) {
   if (!c || !kv || layer >= kv->layers) return fail(YX_ERR_INVALID, "bad arena or layer");
+  if (n && !pages) return fail(YX_ERR_INVALID, "null page list");
   int rc = c->set_device();
   if (rc) return rc;
   const size_t pb = kv->page_bytes();
@@ -896,7 +899,7 @@ int yx_attention_qkv_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* qkv,
 }
 
 int yx_kv_append(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v) {
-  if (!c || !kv) return fail(YX_ERR_INVALID, "null argument");
+  if (!c || !kv || !k || !v) return fail(YX_ERR_INVALID, "null argument");
   int rc = c->set_device();
   if (rc) return rc;
   const size_t bytes = c->rows * kv->hkv * 128 * 4;
@@ -920,7 +923,7 @@ int yx_attention_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* 
 
 int yx_attention(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* out, size_t hq,
                  size_t hkv, size_t window, float scale) {
-  if (!c || !kv) return fail(YX_ERR_INVALID, "null argument");
+  if (!c || !kv || !q || !out) return fail(YX_ERR_INVALID, "null argument");
   int rc = c->set_device();
   if (rc) return rc;
   const size_t bytes = c->rows * hq * 128 * 4;
@@ -948,7 +951,7 @@ int yx_attention_append_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, 
 int yx_attention_append(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v,
                         const float* q, float* out, size_t hq, size_t hkv, size_t window,
                         float scale) {
-  if (!c || !kv) return fail(YX_ERR_INVALID, "null argument");
+  if (!c || !kv || !k || !v || !q || !out) return fail(YX_ERR_INVALID, "null argument");
   int rc = c->set_device();
   if (rc) return rc;
   const size_t qb = c->rows * hq * 128 * 4, kb = c->rows * kv->hkv * 128 * 4;
