@@ -1008,6 +1008,7 @@ int yx_memcpy_d2h(yx_ctx* c, void* dst, const void* src, size_t bytes) {
 
 int yx_dev_copy(yx_ctx* c, void* dst, const void* src, size_t bytes) {
   if (!c) return fail(YX_ERR_INVALID, "null context");
+  if (bytes && (!dst || !src)) return fail(YX_ERR_INVALID, "null buffer");
   if (bytes % 16 || reinterpret_cast<uintptr_t>(dst) % 16 || reinterpret_cast<uintptr_t>(src) % 16)
     return fail(YX_ERR_INVALID, "dev_copy needs 16-byte aligned sizes and pointers");
   int rc = c->set_device();
