@@ -49,3 +49,41 @@ def test_no_device_calls_on_load_and_errors_without_a_device():
         # No GPU here: creating a context fails with a status, not a crash.
         assert lib.yx_ctx_create(0, ctypes.byref(c)) != 0
         assert lib.yx_last_error()
+
+
+def test_allocator_abi_refuses_null_arguments():
+    """The host allocator's entry points return a status (or an empty answer) for null
+    handles and arrays instead of dereferencing them."""
+    lib = _lib.kv_lib()
+    ok = 0
+    assert lib.yx_cache_create(8, 1024, 16, None) != ok
+    assert lib.yx_cache_create(1 << 30, 1024, 1 << 40, ctypes.byref(ctypes.c_void_p())) != ok
+    c = ctypes.c_void_p()
+    assert lib.yx_cache_create(8, 1024, 16, ctypes.byref(c)) == ok
+    try:
+        seq = ctypes.c_uint64(0)
+        reused = ctypes.c_size_t(0)
+        assert lib.yx_cache_begin(None, None, 0, ctypes.byref(seq), ctypes.byref(reused)) != ok
+        assert lib.yx_cache_begin(c, None, 3, ctypes.byref(seq), ctypes.byref(reused)) != ok
+        assert lib.yx_cache_begin(c, None, 0, None, ctypes.byref(reused)) != ok
+        s = lib.yx_cache_new_seq(c)
+        ids = (ctypes.c_uint64 * 1)(s)
+        counts = (ctypes.c_size_t * 1)(2)
+        assert lib.yx_cache_append(c, 1, ids, counts, None) != ok
+        assert lib.yx_cache_append(c, 1, None, counts, None) != ok
+        assert lib.yx_cache_append(None, 0, None, None, None) != ok
+        assert lib.yx_cache_fork(c, s, 0, None) != ok
+        assert lib.yx_cache_truncate(None, s, 0) != ok
+        assert lib.yx_cache_seq_tokens(c, s, None, 4) == 0
+        assert lib.yx_cache_take_copies(c, None, 4) == 0
+        assert lib.yx_cache_free_pages(None) == 0
+        assert lib.yx_cache_new_seq(None) == 0
+        lib.yx_cache_pass_get(None, None, None, None, None, None, None)
+        lib.yx_cache_finish(None, s)
+        lib.yx_cache_free_seq(None, s)
+        # The cache still works.
+        toks = (ctypes.c_uint32 * 2)(5, 6)
+        assert lib.yx_cache_append(c, 1, ids, counts, toks) == ok
+        assert lib.yx_cache_seq_len(c, s) == 2
+    finally:
+        lib.yx_cache_destroy(c)

@@ -333,7 +333,7 @@ int yx_cache_create(size_t pages, size_t max_pos, size_t page_size, yx_cache** o
   if (!out) return fail(YX_ERR_INVALID, "null output");
   if (page_size == 0) return fail(YX_ERR_INVALID, "page size must be positive");
   if (pages > 0xffffffffull) return fail(YX_ERR_INVALID, "page ids are 32-bit");
-  if ((pages * page_size) > 0xffffffffull) return fail(YX_ERR_INVALID, "arena slots are 32-bit");
+  if (pages > 0xffffffffull / page_size) return fail(YX_ERR_INVALID, "arena slots are 32-bit");
   try {
     *out = new yx_cache(pages, max_pos, page_size);
   } catch (...) {
@@ -345,15 +345,21 @@ int yx_cache_create(size_t pages, size_t max_pos, size_t page_size, yx_cache** o
 void yx_cache_destroy(yx_cache* c) { delete c; }
 
 void yx_cache_set_prefix_reuse(yx_cache* c, int on) {
+  if (!c) return;
   c->reuse = on != 0;
   if (!c->reuse) c->clear_prefix_cache();
 }
 
-uint64_t yx_cache_new_seq(yx_cache* c) { return c->insert(Seq{}); }
-void yx_cache_free_seq(yx_cache* c, uint64_t id) { c->free_seq(id); }
-void yx_cache_clear_prefix_cache(yx_cache* c) { c->clear_prefix_cache(); }
+uint64_t yx_cache_new_seq(yx_cache* c) { return c ? c->insert(Seq{}) : 0; }
+void yx_cache_free_seq(yx_cache* c, uint64_t id) {
+  if (c) c->free_seq(id);
+}
+void yx_cache_clear_prefix_cache(yx_cache* c) {
+  if (c) c->clear_prefix_cache();
+}
 
 int yx_cache_begin(yx_cache* c, const uint32_t* prompt, size_t n, uint64_t* id, size_t* reused) {
+  if (!c || !id || !reused || (n && !prompt)) return fail(YX_ERR_INVALID, "null argument");
   try {
     return c->begin(prompt, n, id, reused);
   } catch (...) {
@@ -361,14 +367,19 @@ int yx_cache_begin(yx_cache* c, const uint32_t* prompt, size_t n, uint64_t* id, 
   }
 }
 
-void yx_cache_finish(yx_cache* c, uint64_t id) { c->finish(id); }
+void yx_cache_finish(yx_cache* c, uint64_t id) {
+  if (c) c->finish(id);
+}
 
 size_t yx_cache_seq_len(const yx_cache* c, uint64_t id) {
+  if (!c) return 0;
   auto it = c->seqs.find(id);
   return it == c->seqs.end() ? 0 : it->second.len;
 }
 
 size_t yx_cache_seq_tokens(const yx_cache* c, uint64_t id, uint32_t* out, size_t cap) {
+  if (!c) return 0;
+  if (!out) cap = 0;
   auto it = c->seqs.find(id);
   if (it == c->seqs.end()) return 0;
   const auto& t = it->second.tokens;
@@ -378,6 +389,8 @@ size_t yx_cache_seq_tokens(const yx_cache* c, uint64_t id, uint32_t* out, size_t
 }
 
 size_t yx_cache_seq_pages(const yx_cache* c, uint64_t id, uint32_t* out, size_t cap) {
+  if (!c) return 0;
+  if (!out) cap = 0;
   auto it = c->seqs.find(id);
   if (it == c->seqs.end()) return 0;
   const auto& p = it->second.pages;
@@ -386,17 +399,21 @@ size_t yx_cache_seq_pages(const yx_cache* c, uint64_t id, uint32_t* out, size_t 
   return p.size();
 }
 
-size_t yx_cache_free_pages(const yx_cache* c) { return c->pool.free_list.size(); }
-size_t yx_cache_total_pages(const yx_cache* c) { return c->pool.refs.size(); }
-size_t yx_cache_max_pos(const yx_cache* c) { return c->max_pos; }
-size_t yx_cache_page_size(const yx_cache* c) { return c->page; }
+size_t yx_cache_free_pages(const yx_cache* c) { return c ? c->pool.free_list.size() : 0; }
+size_t yx_cache_total_pages(const yx_cache* c) { return c ? c->pool.refs.size() : 0; }
+size_t yx_cache_max_pos(const yx_cache* c) { return c ? c->max_pos : 0; }
+size_t yx_cache_page_size(const yx_cache* c) { return c ? c->page : 0; }
 uint32_t yx_cache_page_refs(const yx_cache* c, uint32_t page) {
-  return page < c->pool.refs.size() ? c->pool.refs[page] : 0;
+  return c && page < c->pool.refs.size() ? c->pool.refs[page] : 0;
 }
 
-int yx_cache_truncate(yx_cache* c, uint64_t id, size_t len) { return c->truncate(id, len); }
+int yx_cache_truncate(yx_cache* c, uint64_t id, size_t len) {
+  if (!c) return fail(YX_ERR_INVALID, "null cache");
+  return c->truncate(id, len);
+}
 
 int yx_cache_fork(yx_cache* c, uint64_t id, size_t len, uint64_t* out) {
+  if (!c || !out) return fail(YX_ERR_INVALID, "null argument");
   try {
     return c->fork(id, len, out);
   } catch (...) {
@@ -406,6 +423,10 @@ int yx_cache_fork(yx_cache* c, uint64_t id, size_t len, uint64_t* out) {
 
 int yx_cache_append(yx_cache* c, size_t n_items, const uint64_t* ids, const size_t* counts,
                     const uint32_t* tokens) {
+  if (!c || (n_items && (!ids || !counts))) return fail(YX_ERR_INVALID, "null argument");
+  size_t total = 0;
+  for (size_t i = 0; i < n_items; ++i) total += counts[i];
+  if (total && !tokens) return fail(YX_ERR_INVALID, "null tokens");
   try {
     return c->append(n_items, ids, counts, tokens);
   } catch (...) {
@@ -413,12 +434,13 @@ int yx_cache_append(yx_cache* c, size_t n_items, const uint64_t* ids, const size
   }
 }
 
-size_t yx_cache_pass_rows(const yx_cache* c) { return c->ids.size(); }
-size_t yx_cache_pass_npages(const yx_cache* c) { return c->pass_pages.size(); }
-size_t yx_cache_pass_nitems(const yx_cache* c) { return c->last.size(); }
+size_t yx_cache_pass_rows(const yx_cache* c) { return c ? c->ids.size() : 0; }
+size_t yx_cache_pass_npages(const yx_cache* c) { return c ? c->pass_pages.size() : 0; }
+size_t yx_cache_pass_nitems(const yx_cache* c) { return c ? c->last.size() : 0; }
 
 void yx_cache_pass_get(const yx_cache* c, uint32_t* ids, uint32_t* pos, uint32_t* kv_slot,
                        uint32_t* pt_off, uint32_t* pages, size_t* last) {
+  if (!c) return;
   size_t r = c->ids.size();
   if (ids && r) memcpy(ids, c->ids.data(), r * 4);
   if (pos && r) memcpy(pos, c->pos.data(), r * 4);
@@ -429,9 +451,11 @@ void yx_cache_pass_get(const yx_cache* c, uint32_t* ids, uint32_t* pos, uint32_t
   if (last && !c->last.empty()) memcpy(last, c->last.data(), c->last.size() * sizeof(size_t));
 }
 
-size_t yx_cache_pending_copies(const yx_cache* c) { return c->copies.size(); }
+size_t yx_cache_pending_copies(const yx_cache* c) { return c ? c->copies.size() : 0; }
 
 size_t yx_cache_take_copies(yx_cache* c, yx_page_copy* out, size_t cap) {
+  if (!c) return 0;
+  if (!out) cap = 0;
   size_t n = c->copies.size() < cap ? c->copies.size() : cap;
   if (n) memcpy(out, c->copies.data(), n * sizeof(yx_page_copy));
   c->copies.erase(c->copies.begin(), c->copies.begin() + n);
