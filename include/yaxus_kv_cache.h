@@ -7,6 +7,9 @@
  *
  * Conventions: every call returns an int status (YX_OK = 0) unless stated; on error
  * `yx_cache_last_error()` gives a thread-local message. No exception crosses the ABI.
+ * A null handle or a null array that the call would read or write is refused with
+ * YX_ERR_INVALID; calls returning a size or an id return 0 for it and void calls do
+ * nothing.
  * Operations that need pages copied append `(src, dst)` pairs to the cache's pending
  * copy list, whether or not they then succeed (kv.rs:4-7); the caller drains it with
  * `yx_cache_take_copies` and must make the copies, in order, before the next pass.
