@@ -235,6 +235,8 @@ int check_kv(yx_ctx* c, yx_kv* kv, size_t layer) {
 }
 
 // Builds the split-K work list of the current pass for (window, hq, hkv).
+static constexpr uint32_t kFanIn = 32;  // chunks per group the automatic split aims at most
+
 int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) {
   auto key = std::make_tuple(window, hq, hkv);
   auto it = c->plans.find(key);
@@ -339,7 +341,13 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
     // Chunks start on quads of blocks (the waves split them in quads), at most
     // kMaxChunks of them.
     const uint32_t nq = (s.b1 - s.b0 + 3) / 4;
-    const uint32_t cq = static_cast<uint32_t>(std::max<size_t>((cb + 3) / 4, (nq + yx::kMaxChunks - 1) / yx::kMaxChunks));
+    uint32_t cq = static_cast<uint32_t>(std::max<size_t>((cb + 3) / 4, (nq + yx::kMaxChunks - 1) / yx::kMaxChunks));
+    // At most kFanIn chunks per group while chunks stay within the one-tile queue
+    // kernel's 16 quads: a few long sequences would otherwise be cut into many short
+    // chunks (2 blocks per wave) whose merge outweighs the parallelism (B=1, ctx 16384:
+    // 64 chunks of 16 blocks 21.9 us, 32 of 32 blocks 17.3 us).
+    if (c->target_waves == 0)
+      cq = std::max(cq, std::min<uint32_t>(yx::kBalQuads, (nq + kFanIn - 1) / kFanIn));
     if (cq * 4 > 64 * waves)
       return fail(YX_ERR_UNSUPPORTED, "context too long for 256 chunks of the widest work item");
     const uint32_t nch = (nq + cq - 1) / cq;
