@@ -233,29 +233,24 @@ __device__ __forceinline__ void finish_item(const AttnItem& it, uint32_t kh, uin
   __syncthreads();
   if (!last) return;
 
-  // Each thread merges one (row, 4 dims) over the chunks in chunk order, with a
+  // A thread merges one (row, 4 dims) over a range of chunks in chunk order, with a
   // running maximum; the loads of 8 chunks are in flight at a time.
   const size_t base0 = static_cast<size_t>(it.part_base) * hkv + kh;
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const uint32_t idx = threadIdx.x + k * kThreads;
-    const uint32_t lr = idx >> 5, qi = idx & 31;
-    if (lr >= nlog || lr >= kRows) continue;
-    float mt = -INFINITY, lt = 0.0f;
-    float4 o = {0, 0, 0, 0};
-    for (uint32_t c0 = 0; c0 < it.nch; c0 += 8) {
+  auto merge_range = [&](uint32_t lr, uint32_t qi, uint32_t c_begin, uint32_t c_end, float& mt,
+                         float& lt, float4& o) {
+    for (uint32_t c0 = c_begin; c0 < c_end; c0 += 8) {
       float2 ml[8];
       float4 po[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const uint32_t ch = min(c0 + j, it.nch - 1);
+        const uint32_t ch = min(c0 + j, c_end - 1);
         const size_t e = (base0 + static_cast<size_t>(ch) * hkv) * rows_per_slot + lr;
         ml[j] = ld2_coherent(rml, static_cast<uint32_t>(e * 8));
         po[j] = ld4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4));
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        if (c0 + j >= it.nch || !(ml[j].y > 0.0f)) continue;  // past the end, or empty
+        if (c0 + j >= c_end || !(ml[j].y > 0.0f)) continue;  // past the range, or empty
         const float mn = fmaxf(mt, ml[j].x);
         const float r = __builtin_amdgcn_exp2f(mt - mn), wt = __builtin_amdgcn_exp2f(ml[j].x - mn);
         lt = lt * r + ml[j].y * wt;
@@ -266,9 +261,52 @@ __device__ __forceinline__ void finish_item(const AttnItem& it, uint32_t kh, uin
         mt = mn;
       }
     }
+  };
+  auto store_row = [&](uint32_t lr, uint32_t qi, float lt, const float4& o) {
     const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
     const float inv = 1.0f / lt;
     *reinterpret_cast<float4*>(out + rr * qd + h * kD + qi * 4) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+  };
+  if (2 * kRows * 32 <= kThreads && it.nch > 8) {  // uniform
+    // Twice as many threads as (row, 4 dims) pairs and more than one round of loads:
+    // the first half merges the first half of the chunks, the second half the rest, and
+    // the first half then adds the second's result (a fixed order, so the result does
+    // not depend on timing). With 8 chunks or fewer the loads are one round anyway.
+    __shared__ float4 half_o[kRows * 32];
+    __shared__ float2 half_ml[kRows * 32];
+    const uint32_t part = threadIdx.x / (kRows * 32), pi = threadIdx.x % (kRows * 32);
+    const uint32_t lr = pi >> 5, qi = pi & 31;
+    const bool active = part < 2 && lr < nlog;
+    const uint32_t mid = (it.nch + 1) / 2;
+    float mt = -INFINITY, lt = 0.0f;
+    float4 o = {0, 0, 0, 0};
+    if (active) merge_range(lr, qi, part ? mid : 0u, part ? it.nch : mid, mt, lt, o);
+    if (active && part == 1) {
+      half_o[pi] = o;
+      half_ml[pi] = float2{mt, lt};
+    }
+    __syncthreads();
+    if (!active || part != 0) return;
+    const float2 b = half_ml[pi];
+    if (b.y > 0.0f) {
+      const float4 ob = half_o[pi];
+      const float mn = fmaxf(mt, b.x);
+      const float r = __builtin_amdgcn_exp2f(mt - mn), wt = __builtin_amdgcn_exp2f(b.x - mn);
+      lt = lt * r + b.y * wt;
+      o = float4{o.x * r + ob.x * wt, o.y * r + ob.y * wt, o.z * r + ob.z * wt, o.w * r + ob.w * wt};
+    }
+    store_row(lr, qi, lt, o);
+  } else {
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const uint32_t idx = threadIdx.x + k * kThreads;
+      const uint32_t lr = idx >> 5, qi = idx & 31;
+      if (lr >= nlog || lr >= kRows) continue;
+      float mt = -INFINITY, lt = 0.0f;
+      float4 o = {0, 0, 0, 0};
+      merge_range(lr, qi, 0, it.nch, mt, lt, o);
+      store_row(lr, qi, lt, o);
+    }
   }
 }
 
