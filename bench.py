@@ -90,6 +90,7 @@ def cpu_baseline(pr, budget_s=10.0):
         "unit": "GB/s",
         "us_per_layer_step": round(us, 1),
         "cores": threads,
+        "host_cpus": len(os.sched_getaffinity(0)),
         "kind": "port",
         "sample": f"{reps} layer-steps of B=16 ctx 4096 (1 layer, attend only) in {el:.1f} s",
     }
