@@ -425,7 +425,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the paged path shards by request; see DESIGN.md)", file=sys.stderr)
+              "(the paged path shards by request and KV head without exchange)", file=sys.stderr)
         sys.exit(2)
 
     from yaxus_amd import KvCache
