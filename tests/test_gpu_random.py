@@ -10,7 +10,7 @@ from tests.scenario import D, Scenario, close
 
 pytestmark = pytest.mark.gpu
 
-HEADS = [(16, 4), (8, 8), (32, 2), (16, 1), (8, 2), (4, 4)]
+HEADS = [(16, 4), (8, 8), (32, 2), (16, 1), (8, 2), (4, 4), (12, 4), (10, 2), (14, 2), (6, 1)]
 PAGES = [16, 32, 64, 128, 256, 512]
 ROWS = [1, 1, 1, 2, 5, 40]
 
