@@ -122,8 +122,8 @@ def _time_layers(hip, kv, pr, layers, hq, windows, steps, extra=None):
 
     rows = len(pr.meta.pos)
     q = hip.tensor((rows, hq * D))
-    k = hip.tensor((rows, HKV * D))
-    v = hip.tensor((rows, HKV * D))
+    k = hip.tensor((rows, kv.hkv * D))
+    v = hip.tensor((rows, kv.hkv * D))
     out = hip.tensor((rows, hq * D))
     for i, t in enumerate((q, k, v)):
         hip.fill_normal(t.ptr, t.nbytes // 4, False, SEED + 99, i << 32)
@@ -187,7 +187,7 @@ def _time_attention_kernel(hip, kv, pr, layers, hq, steps):
 
     rows = len(pr.meta.pos)
     q, out = hip.tensor((rows, hq * D)), hip.tensor((rows, hq * D))
-    k, v = hip.tensor((rows, HKV * D)), hip.tensor((rows, HKV * D))
+    k, v = hip.tensor((rows, kv.hkv * D)), hip.tensor((rows, kv.hkv * D))
     for i, t in enumerate((q, k, v)):
         hip.fill_normal(t.ptr, t.nbytes // 4, False, SEED + 99, i << 32)
     hip.begin_pass(pr.meta)
@@ -533,7 +533,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_attn_decode_balanced (fused append + attention)",
+            "kernel": "paged_attn_decode_wide<1> (fused append + attention)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -51,13 +51,18 @@ int yx_ctx_destroy(yx_ctx* ctx);
 int yx_sync(yx_ctx* ctx);
 /* Tuning knobs: "attn_target_waves" (waves the split-K work list aims at; 0, the
  * default, means one work item per CU), "attn_max_chunk_blocks" (most 16-key blocks per
- * work item), "attn_max_tiles" (most 8-row MFMA tiles a decode wave holds, 1-4, default 3; a row's
- * q heads always fit one work item),
+ * work item), "attn_max_tiles" (most logical rows, in units of 8 (row, q head) pairs,
+ * one decode work item holds, 1-4, default 4; 3 at most with attn_decode_shape 1 unless
+ * one row's q heads need 4; a row's q heads always fit one work item),
  * "prefill_min_rows" (rows of one sequence from which the prefill kernel is used),
- * "attn_decode_shape" (0, the default: one-tile decode passes whose work items hold at
- * most 64 blocks use the kernel whose waves share a queue of blocks; 1: the kernel with
- * a fixed split of blocks over waves only). Setting an option drops cached work lists.
- * Values are positive; 0 is accepted for attn_target_waves and attn_decode_shape. */
+ * "attn_decode_shape" (0, the default: automatic. Passes of more than 8 logical rows per
+ * work item use the kernel with 16-row tiles and a fixed split of blocks over its waves;
+ * so do one-tile passes whose work items split evenly over the waves or hold more than
+ * 64 blocks; other one-tile passes use the kernel whose waves share a queue of blocks.
+ * 1: the kernels with 8-row tiles and a fixed split only. 2: the 16-row-tile kernel for
+ * every decode pass). Setting an option drops
+ * cached work lists. Values are positive; 0 is accepted for attn_target_waves and
+ * attn_decode_shape. */
 int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
 
 /* Backend::new_kv (lib.rs:118; GPU ops/mod.rs:42-66): `layers` layers of `pages`

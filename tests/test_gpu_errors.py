@@ -113,3 +113,22 @@ def test_rejects_null_device_buffers(hip, kv):
     hip.sync()
     for t in (out, q, kk):
         t.free()
+
+
+def test_python_mirror_rejects_short_device_tensors(hip, kv):
+    """The C ABI takes plain pointers and cannot see a buffer's size; the Python mirror
+    checks device tensors against the pass's rows and the arena's heads (here K/V sized
+    for one KV head against an arena of two) before any launch."""
+    hip.begin_pass(_meta([0, 1], [0, 1], [0, 0], [0]))
+    q, out = hip.tensor((2, 4 * D)), hip.tensor((2, 4 * D))
+    k, v = hip.tensor((2, D)), hip.tensor((2, D))
+    try:
+        with pytest.raises(ValueError, match="k: device tensor"):
+            hip.attend_append(kv, 0, k, v, q, 4, out=out)
+        with pytest.raises(ValueError, match="k: device tensor"):
+            hip.append(kv, 0, k, v)
+        with pytest.raises(ValueError, match="q: device tensor"):
+            hip.attend(kv, 0, q, 8, out=out)
+    finally:
+        for t in (q, out, k, v):
+            t.free()

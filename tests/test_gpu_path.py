@@ -79,7 +79,8 @@ def option(hip, key, value):
 
 
 # attn_decode_shape: 0 = the balanced one-tile kernel where it applies (waves share a
-# queue of quads), 1 = the static-split kernel only.
+# queue of quads) and the 16-row-tile kernel for more logical rows, 1 = the 8-row-tile
+# static-split kernels only.
 @pytest.mark.parametrize("shape", [0, 1])
 @pytest.mark.parametrize("page", [16, 32, 64, 128])
 @pytest.mark.parametrize("window", [0, 100])
@@ -116,9 +117,13 @@ def test_split_count_does_not_change_results(hip, target_waves, shape):
     assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
 
 
-@pytest.mark.parametrize("hq,hkv,k", [(16, 4, 6), (16, 4, 5), (8, 8, 3), (16, 1, 2), (32, 1, 1)])
-def test_verify_rows_are_causal(hip, hq, hkv, k):
-    """Multi-row passes per sequence (speculative verify): rows see keys <= their pos."""
+@pytest.mark.parametrize("shape", [0, 1])
+@pytest.mark.parametrize("hq,hkv,k", [(16, 4, 6), (16, 4, 5), (16, 4, 7), (8, 8, 3), (16, 1, 2),
+                                      (32, 1, 1), (12, 4, 4)])
+def test_verify_rows_are_causal(hip, hq, hkv, k, shape):
+    """Multi-row passes per sequence (speculative verify): rows see keys <= their pos.
+    (16, 4, 7): 28 logical rows, one work item in the 16-row-tile kernel, two in the
+    8-row one."""
     sc = Scenario(hip, pages=128, page=16, hkv=hkv, pool_seed=9)
     seqs = [sc.cache.new_seq() for _ in range(4)]
     sc.prefill(dict(zip(seqs, [40, 513, 7, 260])))
@@ -126,7 +131,8 @@ def test_verify_rows_are_causal(hip, hq, hkv, k):
     sc.store(pr)
     rows = len(pr.meta.pos)
     q = sc.draw(rows * hq * D).reshape(rows, hq * D)
-    got = hip.attend(sc.kv, 0, q, hq, window=0)
+    with option(hip, "attn_decode_shape", shape):
+        got = hip.attend(sc.kv, 0, q, hq, window=0)
     want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
     assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
 
@@ -145,9 +151,10 @@ def test_attention_close_to_f64(hip):
     assert np.abs(got - exact).max() < 2e-5
 
 
+@pytest.mark.parametrize("shape", [0, 1])
 @pytest.mark.parametrize("hq,hkv,k,window", [(16, 4, 1, 0), (16, 4, 5, 0), (16, 4, 6, 50),
                                              (32, 1, 2, 0), (8, 2, 3, 0)])
-def test_fused_append_attention(hip, hq, hkv, k, window):
+def test_fused_append_attention(hip, hq, hkv, k, window, shape):
     """One launch stores the rows' K/V and attends (the append falls back to its own
     kernel when a sequence's rows do not fit one work item: hq=32, hkv=1, k=2)."""
     sc = Scenario(hip, pages=200, page=16, hkv=hkv, pool_seed=4)
@@ -158,7 +165,8 @@ def test_fused_append_attention(hip, hq, hkv, k, window):
     kk = sc.draw(rows * hkv * D).reshape(rows, hkv, D)
     vv = sc.draw(rows * hkv * D).reshape(rows, hkv, D)
     q = sc.draw(rows * hq * D).reshape(rows, hq * D)
-    got = hip.attend_append(sc.kv, 0, kk, vv, q, hq, window=window)
+    with option(hip, "attn_decode_shape", shape):
+        got = hip.attend_append(sc.kv, 0, kk, vv, q, hq, window=window)
     sc.orc[0].store(pr.meta.kv_slot, kk.reshape(rows, -1), vv.reshape(rows, -1))
     want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
     assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
@@ -181,6 +189,49 @@ def test_attention_is_deterministic(hip, shape):
         a = hip.attend(sc.kv, 0, q, hq)
         b = hip.attend(sc.kv, 0, q, hq)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", [0, 1, 2])
+@pytest.mark.parametrize("hq,hkv,k", [(4, 4, 1), (8, 2, 1), (16, 4, 1), (16, 2, 1), (16, 4, 3)])
+def test_merge_of_many_chunks(hip, hq, hkv, k, shape):
+    """Long groups cut into ~100 chunks: the last chunk's workgroup merges them in
+    contiguous ranges over up to 16 thread groups (fewer with more logical rows) and
+    adds the ranges in order. shape 2 forces the 16-row-tile kernel on one-tile passes."""
+    sc = Scenario(hip, pages=12000 // 16 * 2 + 16, page=16, hkv=hkv, pool_seed=21)
+    seqs = [sc.cache.new_seq() for _ in range(2)]
+    sc.prefill(dict(zip(seqs, [12000, 5000])))
+    pr = sc.run_pass([(s, k) for s in seqs])
+    sc.store(pr)
+    rows = len(pr.meta.pos)
+    q = sc.draw(rows * hq * D).reshape(rows, hq * D)
+    with option(hip, "attn_decode_shape", shape), option(hip, "attn_target_waves", 4096):
+        a = hip.attend(sc.kv, 0, q, hq)
+        b = hip.attend(sc.kv, 0, q, hq)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
+    assert close(a, want).all(), f"max abs err {np.abs(a - want).max()}"
+
+
+@pytest.mark.parametrize("shape", [0, 1])
+def test_verify_attention_is_deterministic(hip, shape):
+    """Multi-tile work items (5 rows x 4 q heads): two runs give the same bits, and
+    another split of the groups' blocks into chunks stays within the tolerance."""
+    hq, hkv = 16, 4
+    sc = Scenario(hip, pages=800, page=16, hkv=hkv, pool_seed=18)
+    seqs = [sc.cache.new_seq() for _ in range(6)]
+    sc.prefill(dict(zip(seqs, [4000, 3000, 2047, 100, 1, 555])))
+    pr = sc.run_pass([(s, 5) for s in seqs])
+    sc.store(pr)
+    rows = len(pr.meta.pos)
+    q = sc.draw(rows * hq * D).reshape(rows, hq * D)
+    with option(hip, "attn_decode_shape", shape):
+        a = hip.attend(sc.kv, 0, q, hq)
+        b = hip.attend(sc.kv, 0, q, hq)
+        with option(hip, "attn_target_waves", 4096):
+            c = hip.attend(sc.kv, 0, q, hq)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
+    assert close(a, want).all() and close(c, want).all()
 
 
 @pytest.mark.parametrize("hq,hkv,page,window,chunk", [
@@ -301,12 +352,15 @@ def test_model_attention_two_passes_across_pages(hip, window):
 
 @pytest.mark.parametrize("hq,hkv,lens,k", [
     (16, 4, [1, 300, 17, 1000, 64], 1), (8, 2, [40, 513], 1), (16, 4, [40, 513, 7], 5),
-    (32, 2, [100, 2000], 1), (16, 4, [40, 513, 7], 40), (8, 8, [0, 130], 70)])
+    (32, 2, [100, 2000], 1), (16, 4, [40, 513, 7], 40), (8, 8, [0, 130], 70),
+    (16, 4, [4095], 1), (16, 4, [40, 513, 7], 4)])
 def test_attention_in_one_launch_equals_two(hip, hq, hkv, lens, k):
     """Backend::attention in full gives the same bits (attention output and stored K/V)
     as write_rows then attention as separate calls, and both match the oracle: decode
-    passes in one launch (the decode kernel runs write_rows itself), verify passes (k = 5)
-    as write_rows then attention, prefill passes (k >= 32) as the key heads' write_rows
+    passes in one launch (the decode kernel runs write_rows itself: the queue kernel, or
+    the 16-row-tile kernel for [4095], whose 8-quad work items split evenly over its
+    waves, and for k = 4, 16 logical rows), verify passes of more rows (k = 5) as
+    write_rows then attention, prefill passes (k >= 32) as the key heads' write_rows
     then the prefill kernel, which normalises and rotates its q heads itself."""
     from yaxus_amd.rope import inv_freq, rope_table
 

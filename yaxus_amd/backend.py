@@ -22,6 +22,13 @@ from . import _lib
 from ._lib import check_hip, ptr
 
 
+def _need(t, nbytes, what):
+    """Raises unless device tensor t holds at least nbytes: the kernels take plain
+    pointers, so a short buffer would be read or written past its end."""
+    if t.nbytes < nbytes:
+        raise ValueError(f"{what}: device tensor of {t.nbytes} bytes, {nbytes} needed")
+
+
 class DeviceTensor:
     """A device buffer of a fixed numpy dtype and shape, freed with its context."""
 
@@ -151,6 +158,8 @@ class HipBackend:
     # The K/V store of Backend::attention (backend-cpu lib.rs:378-383)
     def append(self, kv, layer, k, v):
         if isinstance(k, DeviceTensor):
+            _need(k, self.rows * kv.hkv * kv.d * 4, "k")
+            _need(v, self.rows * kv.hkv * kv.d * 4, "v")
             check_hip(self.L.yx_kv_append_dev(self.ctx, kv.h, layer, k.ptr, v.ptr))
             return
         k = np.ascontiguousarray(k, np.float32)
@@ -167,6 +176,8 @@ class HipBackend:
         rope_len = int(rope_cs.shape[1]) if len(rope_cs.shape) == 3 else int(rope_cs.shape[0]) // 2
         if isinstance(qkv, DeviceTensor):
             out = out if out is not None else self.tensor((self.rows, hq * kv.d))
+            _need(qkv, self.rows * (hq + 2 * kv.hkv) * kv.d * 4, "qkv")
+            _need(out, self.rows * hq * kv.d * 4, "q out")
             check_hip(self.L.yx_qk_rope_append_dev(self.ctx, kv.h, layer, qkv.ptr, q_norm.ptr,
                                                    k_norm.ptr, rope_cs.ptr, rope_len, float(eps),
                                                    hq, kv.hkv, out.ptr))
@@ -198,6 +209,8 @@ class HipBackend:
         rope_len = int(rope_cs.shape[1]) if len(rope_cs.shape) == 3 else int(rope_cs.shape[0]) // 2
         if isinstance(qkv, DeviceTensor):
             out = out if out is not None else self.tensor((self.rows, hq * kv.d))
+            _need(qkv, self.rows * (hq + 2 * kv.hkv) * kv.d * 4, "qkv")
+            _need(out, self.rows * hq * kv.d * 4, "out")
             check_hip(self.L.yx_attention_qkv_dev(self.ctx, kv.h, layer, qkv.ptr, q_norm.ptr,
                                                   k_norm.ptr, rope_cs.ptr, rope_len, float(eps),
                                                   out.ptr, hq, kv.hkv, w, scale))
@@ -227,6 +240,8 @@ class HipBackend:
         w = int(window or 0)
         if isinstance(q, DeviceTensor):
             out = out if out is not None else self.tensor((self.rows, hq * kv.d))
+            _need(q, self.rows * hq * kv.d * 4, "q")
+            _need(out, self.rows * hq * kv.d * 4, "out")
             check_hip(self.L.yx_attention_dev(self.ctx, kv.h, layer, q.ptr, out.ptr, hq, kv.hkv,
                                               w, scale))
             return out
@@ -245,6 +260,10 @@ class HipBackend:
         w = int(window or 0)
         if isinstance(q, DeviceTensor):
             out = out if out is not None else self.tensor((self.rows, hq * kv.d))
+            _need(k, self.rows * kv.hkv * kv.d * 4, "k")
+            _need(v, self.rows * kv.hkv * kv.d * 4, "v")
+            _need(q, self.rows * hq * kv.d * 4, "q")
+            _need(out, self.rows * hq * kv.d * 4, "out")
             check_hip(self.L.yx_attention_append_dev(self.ctx, kv.h, layer, k.ptr, v.ptr, q.ptr,
                                                      out.ptr, hq, kv.hkv, w, scale))
             return out

@@ -267,46 +267,48 @@ __device__ __forceinline__ void finish_item(const AttnItem& it, uint32_t kh, uin
     const float inv = 1.0f / lt;
     *reinterpret_cast<float4*>(out + rr * qd + h * kD + qi * 4) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
   };
-  if (2 * kRows * 32 <= kThreads && it.nch > 8) {  // uniform
-    // Twice as many threads as (row, 4 dims) pairs and more than one round of loads:
-    // the first half merges the first half of the chunks, the second half the rest, and
-    // the first half then adds the second's result (a fixed order, so the result does
-    // not depend on timing). With 8 chunks or fewer the loads are one round anyway.
-    __shared__ float4 half_o[kRows * 32];
-    __shared__ float2 half_ml[kRows * 32];
-    const uint32_t part = threadIdx.x / (kRows * 32), pi = threadIdx.x % (kRows * 32);
+  // With more than one round of loads (over 8 chunks) and threads to spare, the chunk
+  // list is cut into `parts` contiguous ranges, each merged by its own nlog * 32
+  // threads; part 0 then adds the others' results in part order through LDS (a fixed
+  // order, so the result does not depend on timing).
+  const uint32_t span = nlog * 32;
+  const uint32_t parts = min(static_cast<uint32_t>(kThreads) / span, (it.nch + 7) / 8);  // uniform
+  if (parts >= 2) {
+    __shared__ float4 part_o_lds[kThreads];
+    __shared__ float2 part_ml_lds[kThreads];
+    const uint32_t part = threadIdx.x / span, pi = threadIdx.x - part * span;
     const uint32_t lr = pi >> 5, qi = pi & 31;
-    const bool active = part < 2 && lr < nlog;
-    const uint32_t mid = (it.nch + 1) / 2;
     float mt = -INFINITY, lt = 0.0f;
     float4 o = {0, 0, 0, 0};
-    if (active) merge_range(lr, qi, part ? mid : 0u, part ? it.nch : mid, mt, lt, o);
-    if (active && part == 1) {
-      half_o[pi] = o;
-      half_ml[pi] = float2{mt, lt};
+    if (part < parts) merge_range(lr, qi, it.nch * part / parts, it.nch * (part + 1) / parts, mt, lt, o);
+    if (part > 0 && part < parts) {
+      part_o_lds[threadIdx.x] = o;
+      part_ml_lds[threadIdx.x] = float2{mt, lt};
     }
     __syncthreads();
-    if (!active || part != 0) return;
-    const float2 b = half_ml[pi];
-    if (b.y > 0.0f) {
-      const float4 ob = half_o[pi];
+    if (part != 0) return;
+    for (uint32_t pp = 1; pp < parts; ++pp) {
+      const float2 b = part_ml_lds[pp * span + pi];
+      if (!(b.y > 0.0f)) continue;
+      const float4 ob = part_o_lds[pp * span + pi];
       const float mn = fmaxf(mt, b.x);
       const float r = __builtin_amdgcn_exp2f(mt - mn), wt = __builtin_amdgcn_exp2f(b.x - mn);
       lt = lt * r + b.y * wt;
       o = float4{o.x * r + ob.x * wt, o.y * r + ob.y * wt, o.z * r + ob.z * wt, o.w * r + ob.w * wt};
+      mt = mn;
     }
     store_row(lr, qi, lt, o);
-  } else {
+    return;
+  }
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const uint32_t idx = threadIdx.x + k * kThreads;
-      const uint32_t lr = idx >> 5, qi = idx & 31;
-      if (lr >= nlog || lr >= kRows) continue;
-      float mt = -INFINITY, lt = 0.0f;
-      float4 o = {0, 0, 0, 0};
-      merge_range(lr, qi, 0, it.nch, mt, lt, o);
-      store_row(lr, qi, lt, o);
-    }
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t idx = threadIdx.x + k * kThreads;
+    const uint32_t lr = idx >> 5, qi = idx & 31;
+    if (lr >= nlog || lr >= kRows) continue;
+    float mt = -INFINITY, lt = 0.0f;
+    float4 o = {0, 0, 0, 0};
+    merge_range(lr, qi, 0, it.nch, mt, lt, o);
+    store_row(lr, qi, lt, o);
   }
 }
 
@@ -583,6 +585,41 @@ struct QkvIn {
   float eps;
 };
 
+// write_rows inside the attention kernel: wave t normalises and rotates logical row t's
+// query head into q_lds[t] (write_rows' arithmetic, the same bits), then (item of the
+// group's last chunk only) row t - nlog's key head, which it stores with the row's
+// value head. Ends with a workgroup barrier after the stores have completed, which
+// orders them and the queries in LDS before every wave's reads.
+template <int kWaves>
+__device__ __forceinline__ void fused_write_rows(const AttnItem& it, uint32_t kh, uint32_t G,
+                                                 uint32_t hq, uint32_t hkv, uint32_t nlog,
+                                                 uint32_t bpp_shift, const uint32_t* pos,
+                                                 const uint32_t* __restrict__ kv_slot,
+                                                 const QkvIn& qi_in, float (*q_lds)[kD],
+                                                 float* qsq, int wave, int lane, _Float16* kw,
+                                                 _Float16* vw) {
+  const uint32_t nk = it.chunk == it.nch - 1 ? it.nrows : 0;
+  const uint32_t qd = hq * kD, kvd = hkv * kD, cols = qd + 2 * kvd;
+  for (uint32_t t = static_cast<uint32_t>(wave); t < nlog + nk; t += kWaves) {
+    float o0, o1;
+    if (t < nlog) {
+      const uint32_t rr = it.r0 + t / G, h = kh * G + t % G;
+      norm_rope_head(qi_in.qkv + static_cast<size_t>(rr) * cols + h * kD, qi_in.q_norm,
+                     qi_in.rope_cs, qi_in.rope_len, pos[rr], qi_in.eps, lane, qsq, o0, o1);
+      q_lds[t][lane] = o0;
+      q_lds[t][lane + 64] = o1;
+    } else {
+      const uint32_t rr = it.r0 + (t - nlog);
+      const float* ks = qi_in.qkv + static_cast<size_t>(rr) * cols + qd + kh * kD;
+      norm_rope_head(ks, qi_in.k_norm, qi_in.rope_cs, qi_in.rope_len, pos[rr], qi_in.eps, lane,
+                     qsq, o0, o1);
+      store_kv_head(o0, o1, ks + kvd, kv_slot[rr], kh, hkv, bpp_shift + 4, lane, kw, vw);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
 // QKV: instead of reading q (and storing knew/vnew), the workgroup normalises and rotates
 // its rows' q heads from qkv into LDS (write_rows' arithmetic, the same bits), and the
 // item of the group's last chunk normalises, rotates and stores the rows' key heads and
@@ -611,29 +648,8 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
 
   if (threadIdx.x == 0) sh.next = kBalWaves;  // quads 0..W-1 go to waves 0..W-1
   if constexpr (QKV) {
-    // Wave t: logical row t's query head, then (last chunk only) row t - nlog's key head.
-    const uint32_t nk = it.chunk == it.nch - 1 ? it.nrows : 0;
-    const uint32_t qd = hq * kD, kvd = hkv * kD, cols = qd + 2 * kvd;
-    for (uint32_t t = static_cast<uint32_t>(wave); t < nlog + nk; t += kBalWaves) {
-      float o0, o1;
-      if (t < nlog) {
-        const uint32_t rr = it.r0 + t / G, h = kh * G + t % G;
-        norm_rope_head(qi_in.qkv + static_cast<size_t>(rr) * cols + h * kD, qi_in.q_norm,
-                       qi_in.rope_cs, qi_in.rope_len, pos[rr], qi_in.eps, lane, sh.qsq[wave], o0, o1);
-        sh.q[t][lane] = o0;
-        sh.q[t][lane + 64] = o1;
-      } else {
-        const uint32_t rr = it.r0 + (t - nlog);
-        const float* ks = qi_in.qkv + static_cast<size_t>(rr) * cols + qd + kh * kD;
-        norm_rope_head(ks, qi_in.k_norm, qi_in.rope_cs, qi_in.rope_len, pos[rr], qi_in.eps, lane,
-                       sh.qsq[wave], o0, o1);
-        store_kv_head(o0, o1, ks + kvd, kv_slot[rr], kh, hkv, bpp_shift + 4, lane, kw, vw);
-      }
-    }
-    // Stores complete, then the barrier orders them (and the queries in LDS) before
-    // every wave's reads.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    fused_write_rows<kBalWaves>(it, kh, G, hq, hkv, nlog, bpp_shift, pos, kv_slot, qi_in, sh.q,
+                                sh.qsq[wave], wave, lane, kw, vw);
   } else if (knew != nullptr && it.chunk == it.nch - 1) {
     fused_append<64 * kBalWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
   } else {
@@ -801,6 +817,238 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
       const float wt = __builtin_amdgcn_exp2f(sh.m[k][lr] - mt);  // 0 for an empty quad
       lt += sh.l[k][lr] * wt;
       const float4 ow = sh.o[k][lr][qi];
+      o.x += ow.x * wt;
+      o.y += ow.y * wt;
+      o.z += ow.z * wt;
+      o.w += ow.w * wt;
+    }
+  });
+}
+
+// Wide multi-tile decode (verify passes and groups of 9-32 logical rows): tiles of 16
+// logical rows, one per MFMA column. q's f16 hi and lo parts are two B operands whose
+// products accumulate into the same S (and P's into the same O), instead of taking two
+// columns per row as in the 8-row tiles: the same MFMA work per logical row, half the
+// softmax arithmetic (no column is duplicated), and, with one-block register sets, a
+// wave fits 256 registers, so two waves run per SIMD. The item's blocks are split over
+// the waves in whole quads (a static split: the result does not depend on timing).
+static constexpr int kWideWaves = 8;
+
+template <int NT, bool QKV>
+struct WideShared {
+  float m[kWideWaves][NT * 16];
+  float l[kWideWaves][NT * 16];
+  float4 o[kWideWaves][NT * 16][kD / 4];
+  uint32_t last;
+};
+template <int NT>
+struct WideShared<NT, true> : WideShared<NT, false> {
+  float q[NT * 16][kD];           // the group's queries, normalised and rotated here
+  float qsq[kWideWaves][kD];      // per-wave scratch of that step
+};
+
+// QKV (one tile only): as in the queue kernel, the workgroup runs write_rows for its
+// rows first (queries into LDS, the last chunk's item stores the rows' K/V).
+template <int NT, bool QKV>
+__global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
+    const AttnItem* __restrict__ items, const uint32_t* pos,
+    const uint32_t* __restrict__ pages, const _Float16* kc, const _Float16* vc,
+    const float* q, float* __restrict__ out,
+    float* __restrict__ part_o, float2* __restrict__ part_ml, uint32_t* __restrict__ counters,
+    const float* __restrict__ knew, const float* __restrict__ vnew,
+    const uint32_t* __restrict__ kv_slot, _Float16* kw, _Float16* vw,  // kw/vw alias kc/vc
+    uint32_t part_o_bytes, uint32_t part_ml_bytes, uint32_t hq, uint32_t hkv,
+    uint32_t bpp_shift, uint32_t window, float scale_log2, QkvIn qi_in) {
+  static_assert(!QKV || NT == 1, "write_rows is fused for one tile only (LDS)");
+  __shared__ WideShared<NT, QKV> sh;
+  const AttnItem it = items[blockIdx.x];
+  const uint32_t kh = blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, g = lane >> 4;
+  const uint32_t G = hq / hkv;
+  const uint32_t nlog = it.nrows * G;  // logical rows in the group (at most NT * 16)
+
+  if constexpr (QKV)
+    fused_write_rows<kWideWaves>(it, kh, G, hq, hkv, nlog, bpp_shift, pos, kv_slot, qi_in, sh.q,
+                                 sh.qsq[wave], wave, lane, kw, vw);
+  else if (knew != nullptr && it.chunk == it.nch - 1)
+    fused_append<64 * kWideWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
+
+  // This wave's share of the item's blocks, [wb0, wb1), in whole quads; at most 64
+  // blocks per wave, one page id per lane.
+  const uint32_t nall = it.blk1 - it.blk0;
+  const uint32_t quads = (nall + 3) / 4;
+  const uint32_t wb0 = it.blk0 + 4 * (quads * wave / kWideWaves);
+  const uint32_t wb1 = min(it.blk1, it.blk0 + 4 * (quads * (wave + 1) / kWideWaves));
+  const uint32_t nblk = wb1 > wb0 ? wb1 - wb0 : 0;
+  const uint32_t bpp_mask = (1u << bpp_shift) - 1u;
+  const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;
+  const uint32_t* pt = pages + it.pt_off;
+  int pid = 0;  // page id of block wb0 + lane
+  if (static_cast<uint32_t>(lane) < nblk) pid = static_cast<int>(pt[(wb0 + lane) >> bpp_shift]);
+  const int key_end = static_cast<int>(wb1 * 16);
+
+  BlockRegs s0, s1;
+  // Loads block b (relative to wb0; wave-uniform) into r; past nblk it reads nothing.
+  auto load_set = [&](BlockRegs& r, uint32_t b) {
+    const bool valid = b < nblk;
+    const uint32_t page = static_cast<uint32_t>(__builtin_amdgcn_readlane(pid, static_cast<int>(valid ? b : 0)));
+    const size_t o = (static_cast<size_t>(page) * hkv + kh) * head_stride +
+                     static_cast<size_t>((wb0 + b) & bpp_mask) * 16 * kD;
+    load_block_buf(r, kc + o, vc + o, valid, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Per tile: this lane's column's row position and key window, and q (clamped to a
+  // valid row, zeroed after the load for columns past the group's rows).
+  int rpos[NT], rlo[NT];
+  float4 qraw[NT][8];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const uint32_t lr = t * 16 + c;
+    const uint32_t lrc = lr < nlog ? lr : 0;
+    const uint32_t rr = it.r0 + lrc / G, h = kh * G + lrc % G;
+    const int p = static_cast<int>(pos[rr]);
+    rpos[t] = lr < nlog ? p : -1;
+    rlo[t] = (window > 0 && p + 1 > static_cast<int>(window)) ? p + 1 - static_cast<int>(window) : 0;
+    const float* qp;
+    if constexpr (QKV) qp = &sh.q[lrc][g * 8];
+    else qp = q + (static_cast<size_t>(rr) * hq + h) * kD + g * 8;
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      qraw[t][2 * pp] = *reinterpret_cast<const float4*>(qp + pp * 32);
+      qraw[t][2 * pp + 1] = *reinterpret_cast<const float4*>(qp + pp * 32 + 4);
+    }
+  }
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  load_set(s0, 0);
+  load_set(s1, 1);
+  half8 qh[NT][4], ql[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const bool has_row = static_cast<uint32_t>(t * 16 + c) < nlog;
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      const float4 a = qraw[t][2 * pp], b = qraw[t][2 * pp + 1];
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = has_row ? x[e] : 0.0f;
+        const _Float16 hi = static_cast<_Float16>(v);
+        qh[t][pp][e] = hi;
+        ql[t][pp][e] = static_cast<_Float16>(v - static_cast<float>(hi));
+      }
+    }
+  }
+
+  float m[NT], l[NT];
+  floatx4 acc[NT][8];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    m[t] = -INFINITY;
+    l[t] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[t][j] = floatx4{0, 0, 0, 0};
+  }
+
+  auto process_set = [&](const BlockRegs& r, uint32_t b) {
+    const int kb0 = static_cast<int>((wb0 + b) * 16) + 4 * g;
+    half4 va[8];  // V^T operand: dims c*8 + j of keys 4g..4g+3
+#pragma unroll
+    for (int j = 0; j < 8; ++j) va[j] = half4{r.v[0][j], r.v[1][j], r.v[2][j], r.v[3][j]};
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      floatx4 sh_ = {0, 0, 0, 0}, sl_ = {0, 0, 0, 0};
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        sh_ = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.k[p], qh[t][p], sh_, 0, 0, 0);
+        sl_ = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.k[p], ql[t][p], sl_, 0, 0, 0);
+      }
+      float x[4];
+      float bmax = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kp = kb0 + i;
+        const bool ok = (kp >= rlo[t]) & (kp <= rpos[t]) & (kp < key_end);
+        x[i] = ok ? (sh_[i] + sl_[i]) * scale_log2 : -INFINITY;
+        bmax = fmaxf(bmax, x[i]);
+      }
+      bmax = max_xor32(max_xor16(bmax));
+      const float mn = fmaxf(m[t], bmax);
+      const bool live = mn != -INFINITY;
+      float pr[4], rs = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pr[i] = live ? __builtin_amdgcn_exp2f(x[i] - mn) : 0.0f;
+        rs += pr[i];
+      }
+      rs = sum_xor32(sum_xor16(rs));
+      if (__builtin_amdgcn_ballot_w64(mn != m[t])) {
+        const float corr = live ? __builtin_amdgcn_exp2f(m[t] - mn) : 1.0f;
+        l[t] *= corr;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[t][j] *= corr;
+      }
+      l[t] += rs;
+      m[t] = mn;
+      half4 ph, pl;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const _Float16 hi = static_cast<_Float16>(pr[e]);
+        ph[e] = hi;
+        pl[e] = static_cast<_Float16>(pr[e] - static_cast<float>(hi));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[j], ph, acc[t][j], 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[j], pl, acc[t][j], 0, 0, 0);
+    }
+  };
+
+  // Whole quads, loads and compute unconditional (blocks past nblk read nothing and are
+  // masked); each load goes two blocks ahead.
+  const uint32_t nq = (nblk + 3) / 4;
+  for (uint32_t qd = 0; qd < nq; ++qd) {
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      BlockRegs& set = (j & 1) ? s1 : s0;
+      process_set(set, 4 * qd + j);
+      load_set(set, 4 * qd + j + 2);
+    }
+  }
+
+  // Each wave's (m, l, O) of its logical rows to LDS; O dims 32g + 8i + j per lane.
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int lr = t * 16 + c;
+    if (g == 0) {
+      sh.m[wave][lr] = m[t];
+      sh.l[wave][lr] = l[t];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sh.o[wave][lr][g * 8 + i * 2] = float4{acc[t][0][i], acc[t][1][i], acc[t][2][i], acc[t][3][i]};
+      sh.o[wave][lr][g * 8 + i * 2 + 1] = float4{acc[t][4][i], acc[t][5][i], acc[t][6][i], acc[t][7][i]};
+    }
+  }
+  __syncthreads();
+
+  finish_item<64 * kWideWaves, NT * 16>(it, kh, G, hq, hkv, nlog, out, part_o, part_ml, counters,
+                                        part_o_bytes, part_ml_bytes, sh.last,
+                                        [&](uint32_t lr, uint32_t qi, float& mt, float& lt, float4& o) {
+    mt = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWideWaves; ++w) mt = fmaxf(mt, sh.m[w][lr]);
+    lt = 0.0f;
+    o = float4{0, 0, 0, 0};
+    if (mt == -INFINITY) return;
+#pragma unroll
+    for (int w = 0; w < kWideWaves; ++w) {
+      const float wt = __builtin_amdgcn_exp2f(sh.m[w][lr] - mt);  // 0 for an empty wave
+      lt += sh.l[w][lr] * wt;
+      const float4 ow = sh.o[w][lr][qi];
       o.x += ow.x * wt;
       o.y += ow.y * wt;
       o.z += ow.z * wt;

@@ -116,6 +116,7 @@ struct AttnPlan {
   int nt = 1;
   bool balanced = false;  // one tile, items of at most 4 * kBalQuads blocks: waves share a queue
   bool small_units = false;  // balanced with items of at most 2 * kBalQuads blocks: 2-block units
+  bool wide = false;  // several tiles: 16-row tiles of the wide kernel instead of 8-row ones
   std::vector<yx::AttnItem> items;
   DevBuf d_items;
   bool fusable = false;  // the append can run inside the attention kernel
@@ -174,8 +175,13 @@ struct yx_ctx {
   int cus = 256;
   long max_chunk_blocks = 1 << 20;
   long prefill_min_rows = 32;
-  long max_tiles = 3;  // a fourth tile does not fit one wave's registers (it spills)
-  long decode_shape = 0;  // 0: balanced one-tile kernel where it applies, 1: static split only
+  // Most 8-row units of logical rows per work item. The wide kernel holds 32 rows in two
+  // 16-row tiles; the static 8-row-tile kernel spills with a fourth tile, so it keeps 3
+  // unless one row's q heads need 4.
+  long max_tiles = 4;
+  // 0: automatic (the queue or the 16-row-tile kernel), 1: 8-row-tile static split only,
+  // 2: the 16-row-tile kernel for every decode pass.
+  long decode_shape = 0;
   bool profiling = false;
   Profile prof[4];
   bool capturing = false;
@@ -287,7 +293,8 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
     return YX_OK;
   }
   size_t nt = (max_rows * G + 7) / 8;
-  nt = std::max<size_t>(1, std::min<size_t>(nt, static_cast<size_t>(c->max_tiles)));
+  const long cap = c->decode_shape != 1 ? c->max_tiles : std::min<long>(c->max_tiles, 3);
+  nt = std::max<size_t>(1, std::min<size_t>(nt, static_cast<size_t>(cap)));
   nt = std::max<size_t>(nt, (G + 7) / 8);  // one row's q heads always fit one work item
   const size_t rows_per_sub = nt * 8 / G;
   if (rows_per_sub == 0) return fail(YX_ERR_UNSUPPORTED, "more than 32 query heads per KV head");
@@ -321,7 +328,9 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   // One workgroup per CU runs at a time for every tile count (8 waves of ~220
   // registers, or 4 of more than 256), so by default the split aims at one work item
   // per CU: more would run in a second round.
-  const size_t waves = nt == 1 ? yx::DecodeWaves<1>::value : yx::DecodeWaves<2>::value;
+  const bool wide = (nt > 1 && c->decode_shape == 0) || c->decode_shape == 2;
+  const size_t waves = nt == 1 ? yx::DecodeWaves<1>::value
+                               : (wide ? yx::kWideWaves : yx::DecodeWaves<2>::value);
   const size_t target_items = c->target_waves > 0
                                   ? std::max<size_t>(1, static_cast<size_t>(c->target_waves) / waves)
                                   : static_cast<size_t>(c->cus);
@@ -335,6 +344,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
 
   AttnPlan plan;
   plan.nt = static_cast<int>(nt);
+  plan.wide = wide;
   size_t slot = 0;
   for (size_t si = 0; si < subs.size(); ++si) {
     const Sub& s = subs[si];
@@ -388,6 +398,17 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   plan.small_units = plan.balanced;
   for (const yx::AttnItem& w : plan.items)
     if (w.blk1 - w.blk0 > 2 * yx::kBalQuads) plan.small_units = false;
+  // One tile: the 16-row-tile kernel's static split of quads over its waves where that
+  // split is exact (every item's quads a multiple of the waves) or the items are too
+  // long for the queue; the queue kernel where waves would otherwise get unequal shares.
+  // (Measured: B=16 ctx 4096, 16-quad items, 25.9 against 26.3 us; cfg4's 32-quad items
+  // 47.7 against 48.4; cfg2's 11-quad items 26.6 against 24.9.)
+  if (nt == 1 && c->decode_shape == 0) {
+    bool exact = true;
+    for (const yx::AttnItem& w : plan.items)
+      if (((w.blk1 - w.blk0 + 3) / 4) % yx::kWideWaves != 0) exact = false;
+    plan.wide = exact || !plan.balanced;
+  }
   plan.slots = slot;
   plan.counters = subs.size();
   if (plan.items.size() > 0x7fffffff) return fail(YX_ERR_UNSUPPORTED, "too many work items");
@@ -424,7 +445,8 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   if (c->capturing && !c->plans.count(std::make_tuple(window, hq, hkv)))
     return fail(YX_ERR_INVALID, "run the call once before capturing it (its work list is uploaded then)");
   if ((rc = build_plan(c, window, hq, hkv, &plan))) return rc;
-  const size_t rps = static_cast<size_t>(plan->nt) * 8;
+  // Logical rows per partial slot: the kernel's tile rows.
+  const size_t rps = plan->wide ? static_cast<size_t>((plan->nt + 1) / 2) * 16 : static_cast<size_t>(plan->nt) * 8;
   if ((rc = c->part_o.ensure(std::max<size_t>(1, plan->slots * hkv * rps * 128 * 4), c->stream)))
     return rc;
   if ((rc = c->part_ml.ensure(std::max<size_t>(1, plan->slots * hkv * rps * 8), c->stream)))
@@ -438,7 +460,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   if (qkv && plan->prefill) {
     // The prefill kernel normalises and rotates its rows' q heads itself; K/V first.
     if ((rc = qk_rope_impl(c, kv, layer, *qkv, hq, nullptr, true))) return rc;
-  } else if (qkv && !(plan->balanced && plan->fusable)) {
+  } else if (qkv && !(plan->fusable && (plan->wide ? plan->nt <= 2 : plan->balanced))) {
     if ((rc = c->io_q.ensure(std::max<size_t>(16, c->rows * hq * 128 * 4), c->stream))) return rc;
     if ((rc = qk_rope_impl(c, kv, layer, *qkv, hq, static_cast<float*>(c->io_q.p)))) return rc;
     q = static_cast<const float*>(c->io_q.p);
@@ -467,6 +489,10 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     YX_HIP(hipGetLastError());
     return prof_end(c, YX_KERNEL_ATTENTION, e0);
   }
+  // write_rows runs in the same launch in the queue kernel and the one-tile wide kernel
+  // only (qkv was cleared above otherwise).
+  if (qkv && !(plan->wide ? plan->nt <= 2 : plan->balanced))
+    return fail(YX_ERR_INVALID, "internal: write_rows cannot be fused here");
   const float scale_log2 = scale * yx::kLog2e;
   dim3 grid(static_cast<unsigned>(plan->items.size()), static_cast<unsigned>(hkv));
   hipEvent_t e0;
@@ -489,7 +515,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
                      kv->k[layer], kv->v[layer], q, out, po, pml, cnt, knew, vnew,                 \
                      static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],       \
                      po_bytes, pml_bytes, H, HK, P, W, scale_log2)
-  if (plan->balanced) {
+  if (plan->balanced && !plan->wide) {
 #define YX_LAUNCH_BAL(QKV, UB, KN, VN, IN)                                                          \
   hipLaunchKernelGGL((yx::paged_attn_decode_balanced<QKV, UB>), grid, dim3(64 * yx::kBalWaves), 0,  \
                      c->stream, items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml,     \
@@ -500,6 +526,16 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     else if (plan->small_units) YX_LAUNCH_BAL(false, 2, knew, vnew, yx::QkvIn{});
     else YX_LAUNCH_BAL(false, 4, knew, vnew, yx::QkvIn{});
 #undef YX_LAUNCH_BAL
+  } else if (plan->wide) {
+#define YX_LAUNCH_WIDE(NT, QKV, KN, VN, IN)                                                         \
+  hipLaunchKernelGGL((yx::paged_attn_decode_wide<NT, QKV>), grid, dim3(64 * yx::kWideWaves), 0,     \
+                     c->stream, items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml,     \
+                     cnt, KN, VN, static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer],        \
+                     kv->v[layer], po_bytes, pml_bytes, H, HK, P, W, scale_log2, IN)
+    if (qkv) YX_LAUNCH_WIDE(1, true, nullptr, nullptr, *qkv);
+    else if (plan->nt <= 2) YX_LAUNCH_WIDE(1, false, knew, vnew, yx::QkvIn{});
+    else YX_LAUNCH_WIDE(2, false, knew, vnew, yx::QkvIn{});
+#undef YX_LAUNCH_WIDE
   } else switch (plan->nt) {
     case 1: YX_LAUNCH_DECODE(1); break;
     case 2: YX_LAUNCH_DECODE(2); break;
@@ -637,7 +673,7 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
   else if (!std::strcmp(key, "attn_max_tiles"))
     c->max_tiles = std::min<long>(value, 4);
   else if (!std::strcmp(key, "attn_decode_shape"))
-    c->decode_shape = std::min<long>(value, 1);
+    c->decode_shape = std::min<long>(value, 2);
   else if (!std::strcmp(key, "prefill_min_rows"))
     c->prefill_min_rows = value;
   else if (!std::strcmp(key, "attn_max_chunk_blocks"))
