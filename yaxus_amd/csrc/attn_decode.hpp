@@ -831,7 +831,7 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
 // columns per row as in the 8-row tiles: the same MFMA work per logical row, half the
 // softmax arithmetic (no column is duplicated), and, with one-block register sets, a
 // wave fits 256 registers, so two waves run per SIMD. The item's blocks are split over
-// the waves in whole quads (a static split: the result does not depend on timing).
+// the waves evenly, to a block (a static split: the result does not depend on timing).
 static constexpr int kWideWaves = 8;
 
 template <int NT, bool QKV>
@@ -875,13 +875,12 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
   else if (knew != nullptr && it.chunk == it.nch - 1)
     fused_append<64 * kWideWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
 
-  // This wave's share of the item's blocks, [wb0, wb1), in whole quads; at most 64
-  // blocks per wave, one page id per lane.
+  // This wave's share of the item's blocks, [wb0, wb1): shares differ by at most one
+  // block; at most 64 blocks per wave, one page id per lane.
   const uint32_t nall = it.blk1 - it.blk0;
-  const uint32_t quads = (nall + 3) / 4;
-  const uint32_t wb0 = it.blk0 + 4 * (quads * wave / kWideWaves);
-  const uint32_t wb1 = min(it.blk1, it.blk0 + 4 * (quads * (wave + 1) / kWideWaves));
-  const uint32_t nblk = wb1 > wb0 ? wb1 - wb0 : 0;
+  const uint32_t wb0 = it.blk0 + nall * wave / kWideWaves;
+  const uint32_t wb1 = it.blk0 + nall * (wave + 1) / kWideWaves;
+  const uint32_t nblk = wb1 - wb0;
   const uint32_t bpp_mask = (1u << bpp_shift) - 1u;
   const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;
   const uint32_t* pt = pages + it.pt_off;
@@ -1007,16 +1006,13 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
     }
   };
 
-  // Whole quads, loads and compute unconditional (blocks past nblk read nothing and are
-  // masked); each load goes two blocks ahead.
-  const uint32_t nq = (nblk + 3) / 4;
-  for (uint32_t qd = 0; qd < nq; ++qd) {
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
-      BlockRegs& set = (j & 1) ? s1 : s0;
-      process_set(set, 4 * qd + j);
-      load_set(set, 4 * qd + j + 2);
-    }
+  // Pairs of blocks, loads and compute unconditional (a block past nblk reads nothing
+  // and is masked); each load goes two blocks ahead.
+  for (uint32_t b = 0; b < nblk; b += 2) {
+    process_set(s0, b);
+    load_set(s0, b + 2);
+    process_set(s1, b + 1);
+    load_set(s1, b + 3);
   }
 
   // Each wave's (m, l, O) of its logical rows to LDS; O dims 32g + 8i + j per lane.

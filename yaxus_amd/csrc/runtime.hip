@@ -398,15 +398,15 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   plan.small_units = plan.balanced;
   for (const yx::AttnItem& w : plan.items)
     if (w.blk1 - w.blk0 > 2 * yx::kBalQuads) plan.small_units = false;
-  // One tile: the 16-row-tile kernel's static split of quads over its waves where that
-  // split is exact (every item's quads a multiple of the waves) or the items are too
+  // One tile: the 16-row-tile kernel's static split of blocks over its waves where that
+  // split is exact (every item's blocks a multiple of the waves) or the items are too
   // long for the queue; the queue kernel where waves would otherwise get unequal shares.
-  // (Measured: B=16 ctx 4096, 16-quad items, 25.9 against 26.3 us; cfg4's 32-quad items
-  // 47.7 against 48.4; cfg2's 11-quad items 26.6 against 24.9.)
+  // (Measured: B=16 ctx 4096, 64-block items, 25.9 against 26.3 us; cfg4's 128-block
+  // items 47.3 against 48.4; cfg2's ~44-block items 25.4 against 24.9.)
   if (nt == 1 && c->decode_shape == 0) {
     bool exact = true;
     for (const yx::AttnItem& w : plan.items)
-      if (((w.blk1 - w.blk0 + 3) / 4) % yx::kWideWaves != 0) exact = false;
+      if ((w.blk1 - w.blk0) % yx::kWideWaves != 0) exact = false;
     plan.wide = exact || !plan.balanced;
   }
   plan.slots = slot;
