@@ -99,10 +99,11 @@ def cpu_baseline(pr, budget_s=10.0):
 def _fill_arena(hip, kv, layers, seed):
     from yaxus_amd._lib import YX_K, YX_V
 
-    per = kv.pages * kv.page_bytes // 2
+    f16 = not getattr(kv, "f32", False)
+    per = kv.pages * kv.page_bytes // (2 if f16 else 4)
     for l in range(layers):
-        hip.fill_normal(kv.layer_ptr(l, YX_K), per, True, seed, (2 * l) * per)
-        hip.fill_normal(kv.layer_ptr(l, YX_V), per, True, seed, (2 * l + 1) * per)
+        hip.fill_normal(kv.layer_ptr(l, YX_K), per, f16, seed, (2 * l) * per)
+        hip.fill_normal(kv.layer_ptr(l, YX_V), per, f16, seed, (2 * l + 1) * per)
 
 
 def _scatter(cache, pool, seed):
@@ -309,7 +310,7 @@ def cfg5_pass(KvCache):
 
 def bench_configs(hip, steps=10, include_long=True, only=None):
     """BASELINE configurations 2-5 at full size (one JSON object per configuration);
-    `only`: a set of names among cfg2, cfg3, cfg4, cfg5 to run (all when None)."""
+    `only`: a set of names among cfg2, cfg3, cfg4, cfg5, f32 to run (all when None)."""
     from yaxus_amd import KvCache
     from yaxus_amd.data import uniform_ints
 
@@ -382,6 +383,18 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
                                    "fork_copies": len(copies), "copy_us_all_layers": round(copy_us, 2),
                                    "host_fork_rollback_us": round(host_us, 1)}
         kv.destroy()
+    if want('f32'):
+        # The headline's pass on an f32 arena (the reference's K/V precision): twice
+        # the bytes, f32 MFMAs.
+        _, pr = build_pass(KvCache)
+        kv = hip.new_kv(layers, POOL, PAGE, HKV, D, f32=True)
+        _fill_arena(hip, kv, layers, SEED)
+        us = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, steps) / layers
+        nbytes = B * CTX * HKV * D * 4 * 2
+        res["f32_arena_b16_ctx4096"] = {"us_per_layer_step": round(us, 2),
+                                        "GBs": round(nbytes / us / 1e3, 1),
+                                        "kv_bytes_per_layer": nbytes}
+        kv.destroy()
     if include_long and want('cfg4'):
         # cfg4: 32 layers, 1 full then 3 sliding (window 2048), repeated.
         cache, pr, pool = cfg4_pass(KvCache)
@@ -417,7 +430,7 @@ def main():
                     help="for rocprofv3: also run a 1 GiB device copy (the byte-counter "
                          "calibration point) and skip the CPU baseline")
     ap.add_argument("--only", default=None,
-                    help="with --configs: comma-separated subset of cfg2,cfg3,cfg4,cfg5")
+                    help="with --configs: comma-separated subset of cfg2,cfg3,cfg4,cfg5,f32")
     ap.add_argument("--configs", action="store_true",
                     help="also measure BASELINE configurations 2-5 at full size (adds ~2 min)")
     ap.add_argument("--no-graph", action="store_true",

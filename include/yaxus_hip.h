@@ -66,7 +66,11 @@ int yx_sync(yx_ctx* ctx);
 int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
 
 /* Backend::new_kv (lib.rs:118; GPU ops/mod.rs:42-66): `layers` layers of `pages`
- * pages of `page_size` tokens (a multiple of 16). dtype YX_DTYPE_F16 only. Zeroed. */
+ * pages of `page_size` tokens (a multiple of 16), zeroed. dtype YX_DTYPE_F16 (binary16,
+ * the fast path) or YX_DTYPE_F32 (the reference's own K/V precision: stores are exact,
+ * attention runs on f32 MFMAs, every pass as split-K decode with at most 16 (row, q
+ * head) pairs per work item, at most 16 q heads per KV head, write_rows as its own
+ * launch). */
 int yx_kv_create(yx_ctx* ctx, size_t layers, size_t pages, size_t page_size, size_t hkv,
                  size_t head_dim, int dtype, yx_kv** out);
 int yx_kv_destroy(yx_ctx* ctx, yx_kv* kv);
@@ -78,7 +82,8 @@ size_t yx_kv_page_bytes(const yx_kv* kv);
  * in every layer, K and V, in list order (a later copy sees an earlier one's result). */
 int yx_kv_copy_pages(yx_ctx* ctx, yx_kv* kv, const uint32_t* src, const uint32_t* dst, size_t n);
 
-/* Raw page contents, `[n][hkv][page_size][128]` binary16 bits, synchronous. */
+/* Raw page contents, `[n][hkv][page_size][128]` binary16 bits (f32 bits for an f32
+ * arena), synchronous. */
 int yx_kv_read_pages(yx_ctx* ctx, yx_kv* kv, size_t layer, const uint32_t* pages, size_t n,
                      void* k_out, void* v_out);
 int yx_kv_write_pages(yx_ctx* ctx, yx_kv* kv, size_t layer, const uint32_t* pages, size_t n,

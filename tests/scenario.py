@@ -17,11 +17,11 @@ D = 128
 
 
 class Scenario:
-    def __init__(self, hip, pages, page, hkv, layers=1, seed=1234, pool_seed=None):
+    def __init__(self, hip, pages, page, hkv, layers=1, seed=1234, pool_seed=None, f32=False):
         self.hip, self.page, self.hkv = hip, page, hkv
         self.cache = KvCache(pages, 1 << 30, page)
-        self.kv = hip.new_kv(layers, pages, page, hkv)
-        self.orc = [OracleArena(pages, page, hkv, D, f16=True) for _ in range(layers)]
+        self.kv = hip.new_kv(layers, pages, page, hkv, f32=f32)
+        self.orc = [OracleArena(pages, page, hkv, D, f16=not f32) for _ in range(layers)]
         self.layers = layers
         self.seed = seed
         self.offset = 0

@@ -1,0 +1,119 @@
+"""The f32 arena (`yx_kv_create` with YX_DTYPE_F32): K/V kept in the reference's own
+precision (CpuBackend::new_kv, crates/yaxus-backend-cpu/src/lib.rs:464-470, holds f32),
+attended by the f32-MFMA decode kernel (exact f32 products, f32 accumulation). Stores
+are bit-exact; attention is within the path's tolerance of the oracle's f32 arena and
+within 1e-5 of the f64 brute force (the reference's own paged-vs-dense bound,
+crates/yaxus-backend-cpu/src/lib.rs:709)."""
+
+import numpy as np
+import pytest
+
+from tests.scenario import D, Scenario, close
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def _check_pages(sc, layer, pages):
+    k, v = sc.kv.read_pages(layer, pages)
+    for i, p in enumerate(pages):
+        ok, ov = sc.orc[layer].page_bits(int(p))
+        assert np.array_equal(k[i], _bits(ok)) and np.array_equal(v[i], _bits(ov)), f"page {p}"
+
+
+@pytest.mark.parametrize("page", [16, 64])
+def test_f32_append_is_exact(hip, page):
+    sc = Scenario(hip, pages=64 * 16 // page + 8, page=page, hkv=4, pool_seed=3, f32=True)
+    seqs = [sc.cache.new_seq() for _ in range(3)]
+    sc.prefill(dict(zip(seqs, [1, 37, 300])))
+    used = sorted({int(p) for s in seqs for p in sc.cache.seq_pages(s)})
+    _check_pages(sc, 0, used)
+    sc.kv.destroy()
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 4), (8, 8), (16, 1), (12, 4)])
+@pytest.mark.parametrize("page,window", [(16, 0), (32, 100), (128, 0)])
+@pytest.mark.parametrize("k", [1, 5])
+def test_f32_decode_and_verify_match_oracle(hip, hq, hkv, page, window, k):
+    sc = Scenario(hip, pages=3000 * 2 // page + 40, page=page, hkv=hkv, pool_seed=7, f32=True)
+    lens = [1, 16, 17, 300, 2999, 64]
+    seqs = [sc.cache.new_seq() for _ in lens]
+    sc.prefill(dict(zip(seqs, lens)))
+    pr = sc.run_pass([(s, k) for s in seqs])
+    rows = len(pr.meta.pos)
+    kk = sc.draw(rows * hkv * D).reshape(rows, hkv, D)
+    vv = sc.draw(rows * hkv * D).reshape(rows, hkv, D)
+    q = sc.draw(rows * hq * D).reshape(rows, hq * D)
+    got = hip.attend_append(sc.kv, 0, kk, vv, q, hq, window=window)
+    sc.orc[0].store(pr.meta.kv_slot, kk.reshape(rows, -1), vv.reshape(rows, -1))
+    want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
+    assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
+    exact = sc.orc[0].attend_f64(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
+    assert np.abs(got - exact).max() < 1e-5
+    used = sorted({int(p) for s in seqs for p in sc.cache.seq_pages(s)})
+    _check_pages(sc, 0, used)
+    sc.kv.destroy()
+
+
+def test_f32_prefill_rows_and_determinism(hip):
+    """Many rows per sequence (a prefill chunk) take the same split-K kernel, 16 logical
+    rows per work item; two runs give the same bits."""
+    hq, hkv = 16, 4
+    sc = Scenario(hip, pages=200, page=16, hkv=hkv, pool_seed=5, f32=True)
+    seqs = [sc.cache.new_seq() for _ in range(3)]
+    sc.prefill(dict(zip(seqs, [0 + 8, 700, 33])))
+    pr = sc.run_pass([(s, 48) for s in seqs])
+    sc.store(pr)
+    rows = len(pr.meta.pos)
+    q = sc.draw(rows * hq * D).reshape(rows, hq * D)
+    a = hip.attend(sc.kv, 0, q, hq)
+    b = hip.attend(sc.kv, 0, q, hq)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
+    assert close(a, want).all(), f"max abs err {np.abs(a - want).max()}"
+    sc.kv.destroy()
+
+
+def test_f32_write_rows_and_attention(hip):
+    """Backend::attention on an f32 arena: write_rows stores the key heads as computed
+    (the oracle's f32 bits) and the raw value heads; q is bit-exact; the attention
+    matches the oracle."""
+    from yaxus_amd.rope import inv_freq, rope_table
+
+    hq, hkv = 16, 4
+    f = inv_freq(D, 10000.0)
+    table = rope_table(f, 1.0, 4096)
+    sc = Scenario(hip, pages=200, page=16, hkv=hkv, pool_seed=9, f32=True)
+    seqs = [sc.cache.new_seq() for _ in range(4)]
+    sc.prefill(dict(zip(seqs, [5, 300, 1000, 40])))
+    pr = sc.run_pass([(s, 1) for s in seqs])
+    rows = len(pr.meta.pos)
+    qkv = sc.draw(rows * (hq + 2 * hkv) * D).reshape(rows, -1)
+    qn, kn = sc.draw(D) * 0.1, sc.draw(D) * 0.1
+    q = hip.qk_rope_append(sc.kv, 0, qkv, qn, kn, table, 1e-6, hq)
+    qo = sc.orc[0].write_rows(qkv, hq, qn, kn, 1e-6, f, 1.0, pr.meta.pos, pr.meta.kv_slot)
+    assert np.array_equal(q.view(np.uint32), qo.view(np.uint32))
+    _check_pages(sc, 0, sorted({int(s) // 16 for s in pr.meta.kv_slot}))
+    got = hip.attention(sc.kv, 0, qkv, qn, kn, table, 1e-6, hq)
+    want = sc.orc[0].attend(qo, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
+    assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
+    sc.kv.destroy()
+
+
+def test_f32_copy_pages(hip):
+    """Copy-on-write of a shared tail page in the f32 arena: the copy is bit-exact."""
+    sc = Scenario(hip, pages=64, page=16, hkv=2, pool_seed=4, f32=True)
+    base = sc.cache.new_seq()
+    sc.prefill({base: 40})
+    copies = []
+    fork = sc.cache.fork(base, 40, copies)
+    assert copies, "a partial tail page is copied"
+    sc.hip.copy_pages(sc.kv, copies)
+    for c in copies:
+        sc.orc[0].copy_page(c.src, c.dst)
+    _check_pages(sc, 0, sorted({c.dst for c in copies} | {c.src for c in copies}))
+    assert fork is not None
+    sc.kv.destroy()

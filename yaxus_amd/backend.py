@@ -60,11 +60,14 @@ class DeviceTensor:
 
 
 class Kv:
-    """The arena of one model: ``layers`` layers of ``pages`` pages (binary16 K/V)."""
+    """The arena of one model: ``layers`` layers of ``pages`` pages (binary16 K/V, or
+    f32 with ``f32=True``)."""
 
-    def __init__(self, backend, handle, layers, pages, page, hkv, d):
+    def __init__(self, backend, handle, layers, pages, page, hkv, d, f32=False):
         self.backend, self.h = backend, handle
         self.layers, self.pages, self.page, self.hkv, self.d = layers, pages, page, hkv, d
+        self.f32 = f32
+        self.bits = np.uint32 if f32 else np.uint16
 
     def layer_ptr(self, layer, which):
         p = ctypes.c_void_p()
@@ -76,9 +79,9 @@ class Kv:
         return self.backend.L.yx_kv_page_bytes(self.h)
 
     def read_pages(self, layer, pages):
-        """(K, V) bits of the pages, each ``[n][hkv][page][d]`` uint16."""
+        """(K, V) bits of the pages, each ``[n][hkv][page][d]`` uint16 (uint32 for f32)."""
         pg = np.ascontiguousarray(pages, dtype=np.uint32)
-        k = np.empty((len(pg), self.hkv, self.page, self.d), np.uint16)
+        k = np.empty((len(pg), self.hkv, self.page, self.d), self.bits)
         v = np.empty_like(k)
         check_hip(self.backend.L.yx_kv_read_pages(self.backend.ctx, self.h, layer, ptr(pg),
                                                   len(pg), ptr(k), ptr(v)))
@@ -86,10 +89,16 @@ class Kv:
 
     def write_pages(self, layer, pages, k, v):
         pg = np.ascontiguousarray(pages, dtype=np.uint32)
-        k = np.ascontiguousarray(k, dtype=np.uint16)
-        v = np.ascontiguousarray(v, dtype=np.uint16)
+        k, v = self._as_bits(k), self._as_bits(v)
+        n = len(pg) * self.hkv * self.page * self.d
+        if k.size != n or v.size != n:
+            raise ValueError("k/v must be [n][hkv][page][d] of the arena's dtype")
         check_hip(self.backend.L.yx_kv_write_pages(self.backend.ctx, self.h, layer, ptr(pg),
                                                    len(pg), ptr(k), ptr(v)))
+
+    def _as_bits(self, a):
+        a = np.ascontiguousarray(a)
+        return a.view(self.bits) if a.dtype.itemsize == np.dtype(self.bits).itemsize else a.astype(self.bits)
 
     def destroy(self):
         if self.h:
@@ -125,11 +134,12 @@ class HipBackend:
         return DeviceTensor(self, shape, dtype)
 
     # Backend::new_kv (lib.rs:118)
-    def new_kv(self, layers, pages, page, hkv, d=128):
+    def new_kv(self, layers, pages, page, hkv, d=128, f32=False):
         h = ctypes.c_void_p()
-        check_hip(self.L.yx_kv_create(self.ctx, layers, pages, page, hkv, d, _lib.YX_DTYPE_F16,
+        check_hip(self.L.yx_kv_create(self.ctx, layers, pages, page, hkv, d,
+                                      _lib.YX_DTYPE_F32 if f32 else _lib.YX_DTYPE_F16,
                                       ctypes.byref(h)))
-        return Kv(self, h, layers, pages, page, hkv, d)
+        return Kv(self, h, layers, pages, page, hkv, d, f32)
 
     # Backend::copy_page (lib.rs:120), batched in list order
     def copy_pages(self, kv, copies):

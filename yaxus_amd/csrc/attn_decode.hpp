@@ -1053,4 +1053,220 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
   });
 }
 
+// ---------------------------------------------------------------------------------
+// f32 arena (the reference's own K/V precision): K and V both `[page][kv_head]
+// [page_size][128]` f32. Same structure as the 16-row-tile kernel (16 logical rows, one
+// per MFMA column; static split of blocks over 8 waves; partials through LDS; split-K
+// hand-off), with v_mfma_f32_16x16x4_f32: exact f32 products, f32 accumulation, no
+// hi/lo split. Operand layouts (lane l, c = l % 16, g = l / 16), chosen so that every
+// load instruction reads whole 64-byte pieces of key rows:
+//   QK, step s = 4j + e (32 steps): lane holds K[key c][16j + 4g + e] and
+//     q[row c][16j + 4g + e]; S^T[key 4g + i][col c] lands in element i of the four
+//     partial sums (steps s % 4). Load j: 64 contiguous bytes of each of the 16 keys.
+//   PV, step (t, m): lane holds V[key 4g + t][dim 64(m / 4) + 4c + m % 4] (A) and
+//     P[key 4g + t][col c] (B); the output lands as dims 64h + 16g + 4i + (0..3) of
+//     column c for h = 0, 1. Load (t, h): 256 contiguous bytes of each of 4 keys.
+struct BlockRegsF32 {
+  float4 k[8];
+  float4 v[8];
+};
+
+__device__ __forceinline__ void load_block_f32(BlockRegsF32& r, const float* kblk, const float* vblk,
+                                               bool valid, int lane) {
+  const int c = lane & 15, g = lane >> 4;
+  const int bytes = valid ? 16 * kD * 4 : 0;
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kblk), 0, bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vblk), 0, bytes, 0x00020000);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    r.k[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, (c * kD + 16 * j + 4 * g) * 4, 0, kNontemporal));
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      r.v[2 * t + h] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, ((4 * g + t) * kD + 64 * h + 4 * c) * 4, 0, kNontemporal));
+}
+
+// Fused append into the f32 arena (the item of the group's last chunk, before its waves
+// read): a plain copy of the rows' K/V of this kv head to their slots.
+template <int kThreads>
+__device__ __forceinline__ void fused_append_f32(const AttnItem& it, uint32_t kh, uint32_t hkv,
+                                                 uint32_t bpp_shift, const float* __restrict__ knew,
+                                                 const float* __restrict__ vnew,
+                                                 const uint32_t* __restrict__ kv_slot, float* kw,
+                                                 float* vw) {
+  const uint32_t page_size = 16u << bpp_shift;
+  for (uint32_t i = threadIdx.x; i < it.nrows * 64; i += kThreads) {
+    const uint32_t row = it.r0 + i / 64, ch = (i / 2) % 32;
+    const bool is_k = (i & 1) == 0;
+    const float* src = (is_k ? knew : vnew) + (static_cast<size_t>(row) * hkv + kh) * kD + ch * 4;
+    const uint32_t slot = kv_slot[row];
+    const uint32_t off = slot & (page_size - 1);
+    const size_t region = (static_cast<size_t>(slot >> (bpp_shift + 4)) * hkv + kh) * page_size * kD;
+    *reinterpret_cast<float4*>((is_k ? kw : vw) + region + off * kD + ch * 4) =
+        *reinterpret_cast<const float4*>(src);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_f32(
+    const AttnItem* __restrict__ items, const uint32_t* pos,
+    const uint32_t* __restrict__ pages, const float* kc, const float* vc,
+    const float* q, float* __restrict__ out,
+    float* __restrict__ part_o, float2* __restrict__ part_ml, uint32_t* __restrict__ counters,
+    const float* __restrict__ knew, const float* __restrict__ vnew,
+    const uint32_t* __restrict__ kv_slot, float* kw, float* vw,  // kw/vw alias kc/vc
+    uint32_t part_o_bytes, uint32_t part_ml_bytes, uint32_t hq, uint32_t hkv,
+    uint32_t bpp_shift, uint32_t window, float scale_log2) {
+  __shared__ WideShared<1, false> sh;
+  const AttnItem it = items[blockIdx.x];
+  const uint32_t kh = blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, g = lane >> 4;
+  const uint32_t G = hq / hkv;
+  const uint32_t nlog = it.nrows * G;  // logical rows in the group (at most 16)
+
+  if (knew != nullptr && it.chunk == it.nch - 1)
+    fused_append_f32<64 * kWideWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
+
+  const uint32_t nall = it.blk1 - it.blk0;
+  const uint32_t wb0 = it.blk0 + nall * wave / kWideWaves;
+  const uint32_t wb1 = it.blk0 + nall * (wave + 1) / kWideWaves;
+  const uint32_t nblk = wb1 - wb0;
+  const uint32_t bpp_mask = (1u << bpp_shift) - 1u;
+  const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;
+  const uint32_t* pt = pages + it.pt_off;
+  int pid = 0;  // page id of block wb0 + lane
+  if (static_cast<uint32_t>(lane) < nblk) pid = static_cast<int>(pt[(wb0 + lane) >> bpp_shift]);
+  const int key_end = static_cast<int>(wb1 * 16);
+
+  BlockRegsF32 s0, s1;
+  auto load_set = [&](BlockRegsF32& r, uint32_t b) {
+    const bool valid = b < nblk;
+    const uint32_t page = static_cast<uint32_t>(__builtin_amdgcn_readlane(pid, static_cast<int>(valid ? b : 0)));
+    const size_t o = (static_cast<size_t>(page) * hkv + kh) * head_stride +
+                     static_cast<size_t>((wb0 + b) & bpp_mask) * 16 * kD;
+    load_block_f32(r, kc + o, vc + o, valid, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // This lane's column: its row position, key window and q (dims 16j + 4g + 0..3).
+  const uint32_t lr = c;
+  const bool has_row = lr < nlog;
+  const uint32_t lrc = has_row ? lr : 0;
+  const uint32_t rr = it.r0 + lrc / G, h = kh * G + lrc % G;
+  const int p0 = static_cast<int>(pos[rr]);
+  const int rpos = has_row ? p0 : -1;
+  const int rlo = (window > 0 && p0 + 1 > static_cast<int>(window)) ? p0 + 1 - static_cast<int>(window) : 0;
+  float4 qv[8];
+  {
+    const float* qp = q + (static_cast<size_t>(rr) * hq + h) * kD + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qv[j] = *reinterpret_cast<const float4*>(qp + 16 * j);
+  }
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  load_set(s0, 0);
+  load_set(s1, 1);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (!has_row) qv[j] = float4{0, 0, 0, 0};
+
+  float m = -INFINITY, l = 0.0f;
+  floatx4 acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = floatx4{0, 0, 0, 0};
+
+  auto process_set = [&](const BlockRegsF32& r, uint32_t b) {
+    const int kb0 = static_cast<int>((wb0 + b) * 16) + 4 * g;
+    floatx4 sp[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sp[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(r.k[j].x, qv[j].x, sp[0], 0, 0, 0);
+      sp[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(r.k[j].y, qv[j].y, sp[1], 0, 0, 0);
+      sp[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(r.k[j].z, qv[j].z, sp[2], 0, 0, 0);
+      sp[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(r.k[j].w, qv[j].w, sp[3], 0, 0, 0);
+    }
+    float x[4];
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kp = kb0 + i;
+      const bool ok = (kp >= rlo) & (kp <= rpos) & (kp < key_end);
+      x[i] = ok ? ((sp[0][i] + sp[1][i]) + (sp[2][i] + sp[3][i])) * scale_log2 : -INFINITY;
+      bmax = fmaxf(bmax, x[i]);
+    }
+    bmax = max_xor32(max_xor16(bmax));
+    const float mn = fmaxf(m, bmax);
+    const bool live = mn != -INFINITY;
+    float pr[4], rs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pr[i] = live ? __builtin_amdgcn_exp2f(x[i] - mn) : 0.0f;
+      rs += pr[i];
+    }
+    rs = sum_xor32(sum_xor16(rs));
+    if (__builtin_amdgcn_ballot_w64(mn != m)) {
+      const float corr = live ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
+      l *= corr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] *= corr;
+    }
+    l += rs;
+    m = mn;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) {
+        const float4 vv = r.v[2 * t + mm / 4];
+        const float a = (mm % 4 == 0) ? vv.x : (mm % 4 == 1) ? vv.y : (mm % 4 == 2) ? vv.z : vv.w;
+        acc[mm] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, pr[t], acc[mm], 0, 0, 0);
+      }
+    }
+  };
+
+  for (uint32_t b = 0; b < nblk; b += 2) {
+    process_set(s0, b);
+    load_set(s0, b + 2);
+    process_set(s1, b + 1);
+    load_set(s1, b + 3);
+  }
+
+  if (g == 0) {
+    sh.m[wave][c] = m;
+    sh.l[wave][c] = l;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    sh.o[wave][c][4 * g + i] = float4{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
+    sh.o[wave][c][16 + 4 * g + i] = float4{acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
+  }
+  __syncthreads();
+
+  finish_item<64 * kWideWaves, 16>(it, kh, G, hq, hkv, nlog, out, part_o, part_ml, counters,
+                                   part_o_bytes, part_ml_bytes, sh.last,
+                                   [&](uint32_t lr2, uint32_t qi, float& mt, float& lt, float4& o) {
+    mt = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWideWaves; ++w) mt = fmaxf(mt, sh.m[w][lr2]);
+    lt = 0.0f;
+    o = float4{0, 0, 0, 0};
+    if (mt == -INFINITY) return;
+#pragma unroll
+    for (int w = 0; w < kWideWaves; ++w) {
+      const float wt = __builtin_amdgcn_exp2f(sh.m[w][lr2] - mt);
+      lt += sh.l[w][lr2] * wt;
+      const float4 ow = sh.o[w][lr2][qi];
+      o.x += ow.x * wt;
+      o.y += ow.y * wt;
+      o.z += ow.z * wt;
+      o.w += ow.w * wt;
+    }
+  });
+}
+
 }  // namespace yx

@@ -1,5 +1,6 @@
 // K/V store, page copy and data-fill kernels for the paged arena.
 //
+// Arena layout per layer, f32: K and V both `[page][kv_head][page_size][128]`.
 // Arena layout per layer, binary16: V is `[page][kv_head][page_size][128]`; K is the
 // same but each 16-key block of a (page, kv head) is stored `[4][16 keys][32 dims]`:
 // dim d of key k of the block sits at (d / 32) * 512 + k * 32 + d % 32. That is the
@@ -45,6 +46,25 @@ __global__ __launch_bounds__(256) void kv_append_f16(const float* __restrict__ k
           static_cast<_Float16>(a.w), static_cast<_Float16>(b.x), static_cast<_Float16>(b.y),
           static_cast<_Float16>(b.z), static_cast<_Float16>(b.w)};
   *reinterpret_cast<h8*>(dst) = o;
+}
+
+// The same store into an f32 arena (K and V both `[page][kv_head][page_size][128]`):
+// one thread per 4 consecutive dims of one (row, kv head), a 16-byte copy.
+__global__ __launch_bounds__(256) void kv_append_f32(const float* __restrict__ k,
+                                                     const float* __restrict__ v,
+                                                     const uint32_t* __restrict__ kv_slot,
+                                                     float* __restrict__ kc, float* __restrict__ vc,
+                                                     uint32_t rows, uint32_t hkv, uint32_t page_size) {
+  const uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t per_row = hkv * 32;
+  if (tid >= rows * per_row) return;
+  const uint32_t row = tid / per_row, rem = tid % per_row, h = rem / 32, ch = rem % 32;
+  const float* src = (blockIdx.y == 0 ? k : v) + (static_cast<size_t>(row) * hkv + h) * 128 + ch * 4;
+  const uint32_t slot = kv_slot[row];
+  const uint32_t page = slot / page_size, off = slot % page_size;
+  float* dst = (blockIdx.y == 0 ? kc : vc) + (static_cast<size_t>(page) * hkv + h) * page_size * 128 +
+               off * 128 + ch * 4;
+  *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(src);
 }
 
 // Plain streaming copy (also the calibration kernel for HBM byte counters).

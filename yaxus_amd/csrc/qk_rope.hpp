@@ -73,6 +73,20 @@ __device__ __forceinline__ void store_kv_head(float k0, float k1, const float* _
   }
 }
 
+// The same into an f32 arena (`[page][kv_head][page_size][128]`, K like V): stored as
+// computed.
+__device__ __forceinline__ void store_kv_head(float k0, float k1, const float* __restrict__ vsrc,
+                                              uint32_t slot, uint32_t kh, uint32_t hkv,
+                                              uint32_t page_shift, uint32_t lane, float* kc,
+                                              float* vc) {
+  const uint32_t off = slot & ((1u << page_shift) - 1u);
+  const size_t row = (((static_cast<size_t>(slot >> page_shift) * hkv + kh) * 128) << page_shift) + off * 128;
+  kc[row + lane] = k0;
+  kc[row + lane + 64] = k1;
+  if (lane < 32)  // the value row: 32 lanes of 16 bytes
+    *reinterpret_cast<float4*>(vc + row + lane * 4) = *reinterpret_cast<const float4*>(vsrc + lane * 4);
+}
+
 // write_rows over a whole pass: the pass's head vectors (per row its hq query heads,
 // then its hkv key heads, or the key heads only; vector i = row i / heads) in
 // workgroups of kRopeVecs.
@@ -87,11 +101,13 @@ __device__ __forceinline__ void store_kv_head(float k0, float k1, const float* _
 static constexpr int kRopeVecs = 16;  // 16: 18.0 us at 4096 rows; 32: 19.1; 64: 24.6
 static constexpr int kRopeThreads = 256;
 
+// T: the arena's element type (_Float16 or float).
+template <typename T>
 __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_append(
     const float* __restrict__ qkv, const float* __restrict__ q_norm,
     const float* __restrict__ k_norm, const float* __restrict__ rope_cs, uint32_t rope_len,
     float eps, const uint32_t* __restrict__ pos, const uint32_t* __restrict__ kv_slot,
-    _Float16* __restrict__ kc, _Float16* __restrict__ vc, float* __restrict__ q_out,
+    T* __restrict__ kc, T* __restrict__ vc, float* __restrict__ q_out,
     uint32_t hq, uint32_t hkv, uint32_t page_shift, uint32_t nvec, uint32_t first) {
 #pragma clang fp contract(off)
   __shared__ float xs[kRopeVecs][129];

@@ -116,7 +116,8 @@ struct AttnPlan {
   int nt = 1;
   bool balanced = false;  // one tile, items of at most 4 * kBalQuads blocks: waves share a queue
   bool small_units = false;  // balanced with items of at most 2 * kBalQuads blocks: 2-block units
-  bool wide = false;  // several tiles: 16-row tiles of the wide kernel instead of 8-row ones
+  bool wide = false;  // 16-row tiles (the wide kernel) instead of 8-row ones
+  bool f32 = false;   // the f32-arena kernel
   std::vector<yx::AttnItem> items;
   DevBuf d_items;
   bool fusable = false;  // the append can run inside the attention kernel
@@ -149,9 +150,12 @@ __global__ __launch_bounds__(256) void kv_copy_pages_list(CopyList list,
 
 struct yx_kv {
   size_t layers, pages, page, hkv, d;
-  std::vector<_Float16*> k, v;
+  bool f32 = false;  // f32 K/V (K in V's layout) instead of binary16
+  std::vector<_Float16*> k, v;  // per layer; float* when f32
   DevBuf bases;  // 2 * layers pointers for the copy kernel
-  size_t page_bytes() const { return hkv * page * d * 2; }
+  size_t page_bytes() const { return hkv * page * d * (f32 ? 4 : 2); }
+  float* kf(size_t l) const { return reinterpret_cast<float*>(k[l]); }
+  float* vf(size_t l) const { return reinterpret_cast<float*>(v[l]); }
 };
 
 struct yx_ctx {
@@ -167,7 +171,7 @@ struct yx_ctx {
   uint32_t max_page = 0, max_slot = 0;
   DevBuf d_pos, d_slot, d_pages;
   bool have_pass = false;
-  std::map<std::tuple<size_t, size_t, size_t>, AttnPlan> plans;
+  std::map<std::tuple<size_t, size_t, size_t, bool>, AttnPlan> plans;  // (window, hq, hkv, f32)
   // scratch
   DevBuf part_o, part_ml, counters, io_a, io_b, io_c, io_q;
   // options
@@ -243,8 +247,10 @@ int check_kv(yx_ctx* c, yx_kv* kv, size_t layer) {
 // Builds the split-K work list of the current pass for (window, hq, hkv).
 static constexpr uint32_t kFanIn = 32;  // chunks per group the automatic split aims at most
 
-int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) {
-  auto key = std::make_tuple(window, hq, hkv);
+// f32: the plan of the f32-arena kernel (split-K decode for every pass, 16 logical rows
+// per work item).
+int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, AttnPlan** out) {
+  auto key = std::make_tuple(window, hq, hkv, f32);
   auto it = c->plans.find(key);
   if (it != c->plans.end()) {
     *out = &it->second;
@@ -253,7 +259,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   const size_t G = hq / hkv;
   uint32_t max_rows = 0;
   for (const Group& g : c->groups) max_rows = std::max(max_rows, g.n);
-  if (max_rows >= static_cast<uint32_t>(c->prefill_min_rows)) {
+  if (!f32 && max_rows >= static_cast<uint32_t>(c->prefill_min_rows)) {
     // Tiles of kPrefillRows logical rows: consecutive rows of one sequence.
     AttnPlan plan;
     plan.prefill = true;
@@ -293,9 +299,10 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
     return YX_OK;
   }
   size_t nt = (max_rows * G + 7) / 8;
-  const long cap = c->decode_shape != 1 ? c->max_tiles : std::min<long>(c->max_tiles, 3);
+  const long cap = f32 ? 2 : c->decode_shape != 1 ? c->max_tiles : std::min<long>(c->max_tiles, 3);
   nt = std::max<size_t>(1, std::min<size_t>(nt, static_cast<size_t>(cap)));
   nt = std::max<size_t>(nt, (G + 7) / 8);  // one row's q heads always fit one work item
+  if (f32 && nt > 2) return fail(YX_ERR_UNSUPPORTED, "f32 arena: more than 16 query heads per KV head");
   const size_t rows_per_sub = nt * 8 / G;
   if (rows_per_sub == 0) return fail(YX_ERR_UNSUPPORTED, "more than 32 query heads per KV head");
 
@@ -328,7 +335,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   // One workgroup per CU runs at a time for every tile count (8 waves of ~220
   // registers, or 4 of more than 256), so by default the split aims at one work item
   // per CU: more would run in a second round.
-  const bool wide = (nt > 1 && c->decode_shape == 0) || c->decode_shape == 2;
+  const bool wide = f32 || (nt > 1 && c->decode_shape == 0) || c->decode_shape == 2;
   const size_t waves = nt == 1 ? yx::DecodeWaves<1>::value
                                : (wide ? yx::kWideWaves : yx::DecodeWaves<2>::value);
   const size_t target_items = c->target_waves > 0
@@ -392,7 +399,8 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
       if (w.blk0 * 16 > pmin) plan.fusable = false;
     }
   }
-  plan.balanced = nt == 1 && c->decode_shape == 0;
+  plan.f32 = f32;
+  plan.balanced = !f32 && nt == 1 && c->decode_shape == 0;
   for (const yx::AttnItem& w : plan.items)
     if (w.blk1 - w.blk0 > 4 * yx::kBalQuads) plan.balanced = false;
   plan.small_units = plan.balanced;
@@ -403,7 +411,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, AttnPlan** out) 
   // long for the queue; the queue kernel where waves would otherwise get unequal shares.
   // (Measured: B=16 ctx 4096, 64-block items, 25.9 against 26.3 us; cfg4's 128-block
   // items 47.3 against 48.4; cfg2's ~44-block items 25.4 against 24.9.)
-  if (nt == 1 && c->decode_shape == 0) {
+  if (!f32 && nt == 1 && c->decode_shape == 0) {
     bool exact = true;
     for (const yx::AttnItem& w : plan.items)
       if ((w.blk1 - w.blk0) % yx::kWideWaves != 0) exact = false;
@@ -442,9 +450,9 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   if (c->rows == 0) return YX_OK;
   if (!out || (!q && !qkv)) return fail(YX_ERR_INVALID, "null q or out");
   AttnPlan* plan;
-  if (c->capturing && !c->plans.count(std::make_tuple(window, hq, hkv)))
+  if (c->capturing && !c->plans.count(std::make_tuple(window, hq, hkv, kv->f32)))
     return fail(YX_ERR_INVALID, "run the call once before capturing it (its work list is uploaded then)");
-  if ((rc = build_plan(c, window, hq, hkv, &plan))) return rc;
+  if ((rc = build_plan(c, window, hq, hkv, kv->f32, &plan))) return rc;
   // Logical rows per partial slot: the kernel's tile rows.
   const size_t rps = plan->wide ? static_cast<size_t>((plan->nt + 1) / 2) * 16 : static_cast<size_t>(plan->nt) * 8;
   if ((rc = c->part_o.ensure(std::max<size_t>(1, plan->slots * hkv * rps * 128 * 4), c->stream)))
@@ -460,7 +468,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   if (qkv && plan->prefill) {
     // The prefill kernel normalises and rotates its rows' q heads itself; K/V first.
     if ((rc = qk_rope_impl(c, kv, layer, *qkv, hq, nullptr, true))) return rc;
-  } else if (qkv && !(plan->fusable && (plan->wide ? plan->nt <= 2 : plan->balanced))) {
+  } else if (qkv && (plan->f32 || !(plan->fusable && (plan->wide ? plan->nt <= 2 : plan->balanced)))) {
     if ((rc = c->io_q.ensure(std::max<size_t>(16, c->rows * hq * 128 * 4), c->stream))) return rc;
     if ((rc = qk_rope_impl(c, kv, layer, *qkv, hq, static_cast<float*>(c->io_q.p)))) return rc;
     q = static_cast<const float*>(c->io_q.p);
@@ -491,7 +499,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   }
   // write_rows runs in the same launch in the queue kernel and the one-tile wide kernel
   // only (qkv was cleared above otherwise).
-  if (qkv && !(plan->wide ? plan->nt <= 2 : plan->balanced))
+  if (qkv && (plan->f32 || !(plan->wide ? plan->nt <= 2 : plan->balanced)))
     return fail(YX_ERR_INVALID, "internal: write_rows cannot be fused here");
   const float scale_log2 = scale * yx::kLog2e;
   dim3 grid(static_cast<unsigned>(plan->items.size()), static_cast<unsigned>(hkv));
@@ -515,7 +523,12 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
                      kv->k[layer], kv->v[layer], q, out, po, pml, cnt, knew, vnew,                 \
                      static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],       \
                      po_bytes, pml_bytes, H, HK, P, W, scale_log2)
-  if (plan->balanced && !plan->wide) {
+  if (plan->f32) {
+    hipLaunchKernelGGL(yx::paged_attn_decode_f32, grid, dim3(64 * yx::kWideWaves), 0, c->stream,
+                       items, pos, pages, kv->kf(layer), kv->vf(layer), q, out, po, pml, cnt, knew,
+                       vnew, static_cast<const uint32_t*>(c->d_slot.p), kv->kf(layer),
+                       kv->vf(layer), po_bytes, pml_bytes, H, HK, P, W, scale_log2);
+  } else if (plan->balanced && !plan->wide) {
 #define YX_LAUNCH_BAL(QKV, UB, KN, VN, IN)                                                          \
   hipLaunchKernelGGL((yx::paged_attn_decode_balanced<QKV, UB>), grid, dim3(64 * yx::kBalWaves), 0,  \
                      c->stream, items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml,     \
@@ -556,10 +569,18 @@ int append_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float*
   dim3 grid(static_cast<unsigned>((threads + 255) / 256), 2);
   hipEvent_t e0;
   if ((rc = prof_begin(c, YX_KERNEL_APPEND, &e0))) return rc;
-  hipLaunchKernelGGL(yx::kv_append_f16, grid, dim3(256), 0, c->stream, k, v,
-                     static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],
-                     static_cast<uint32_t>(c->rows), static_cast<uint32_t>(kv->hkv),
-                     static_cast<uint32_t>(kv->page));
+  if (kv->f32) {
+    dim3 grid32(static_cast<unsigned>((threads * 2 + 255) / 256), 2);
+    hipLaunchKernelGGL(yx::kv_append_f32, grid32, dim3(256), 0, c->stream, k, v,
+                       static_cast<const uint32_t*>(c->d_slot.p), kv->kf(layer), kv->vf(layer),
+                       static_cast<uint32_t>(c->rows), static_cast<uint32_t>(kv->hkv),
+                       static_cast<uint32_t>(kv->page));
+  } else {
+    hipLaunchKernelGGL(yx::kv_append_f16, grid, dim3(256), 0, c->stream, k, v,
+                       static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],
+                       static_cast<uint32_t>(c->rows), static_cast<uint32_t>(kv->hkv),
+                       static_cast<uint32_t>(kv->page));
+  }
   YX_HIP(hipGetLastError());
   return prof_end(c, YX_KERNEL_APPEND, e0);
 }
@@ -587,12 +608,20 @@ int qk_rope_impl(yx_ctx* c, yx_kv* kv, size_t layer, const yx::QkvIn& in, size_t
   hipEvent_t e0;
   int rc;
   if ((rc = prof_begin(c, YX_KERNEL_QK_ROPE, &e0))) return rc;
-  hipLaunchKernelGGL(yx::qk_norm_rope_append, grid, dim3(yx::kRopeThreads), 0, c->stream, in.qkv,
-                     in.q_norm, in.k_norm, in.rope_cs, in.rope_len, in.eps,
-                     static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_slot.p),
-                     kv->k[layer], kv->v[layer], q_out, static_cast<uint32_t>(hq),
-                     static_cast<uint32_t>(hkv), page_shift, static_cast<uint32_t>(nvec),
-                     static_cast<uint32_t>(kv_only ? hq : 0));
+  if (kv->f32)
+    hipLaunchKernelGGL(yx::qk_norm_rope_append<float>, grid, dim3(yx::kRopeThreads), 0, c->stream,
+                       in.qkv, in.q_norm, in.k_norm, in.rope_cs, in.rope_len, in.eps,
+                       static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_slot.p),
+                       kv->kf(layer), kv->vf(layer), q_out, static_cast<uint32_t>(hq),
+                       static_cast<uint32_t>(hkv), page_shift, static_cast<uint32_t>(nvec),
+                       static_cast<uint32_t>(kv_only ? hq : 0));
+  else
+    hipLaunchKernelGGL(yx::qk_norm_rope_append<_Float16>, grid, dim3(yx::kRopeThreads), 0, c->stream,
+                       in.qkv, in.q_norm, in.k_norm, in.rope_cs, in.rope_len, in.eps,
+                       static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_slot.p),
+                       kv->k[layer], kv->v[layer], q_out, static_cast<uint32_t>(hq),
+                       static_cast<uint32_t>(hkv), page_shift, static_cast<uint32_t>(nvec),
+                       static_cast<uint32_t>(kv_only ? hq : 0));
   YX_HIP(hipGetLastError());
   return prof_end(c, YX_KERNEL_QK_ROPE, e0);
 }
@@ -689,7 +718,7 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
 int yx_kv_create(yx_ctx* c, size_t layers, size_t pages, size_t page_size, size_t hkv,
                  size_t head_dim, int dtype, yx_kv** out) {
   if (!c || !out) return fail(YX_ERR_INVALID, "null argument");
-  if (dtype != YX_DTYPE_F16) return fail(YX_ERR_UNSUPPORTED, "the device arena holds binary16 K/V only");
+  if (dtype != YX_DTYPE_F16 && dtype != YX_DTYPE_F32) return fail(YX_ERR_UNSUPPORTED, "dtype must be f16 or f32");
   if (head_dim != 128) return fail(YX_ERR_UNSUPPORTED, "head_dim must be 128");
   if (page_size < 16 || (page_size & (page_size - 1)) != 0)
     return fail(YX_ERR_UNSUPPORTED, "page size must be a power of two, at least 16");
@@ -703,6 +732,7 @@ int yx_kv_create(yx_ctx* c, size_t layers, size_t pages, size_t page_size, size_
   kv->page = page_size;
   kv->hkv = hkv;
   kv->d = head_dim;
+  kv->f32 = dtype == YX_DTYPE_F32;
   const size_t bytes = pages * kv->page_bytes();
   std::vector<void*> bases;
   for (size_t l = 0; l < layers; ++l) {
@@ -825,7 +855,15 @@ static int page_io(yx_ctx* c, yx_kv* kv, size_t layer, const uint32_t* pages, si
     if (pages[i] >= kv->pages) return fail(YX_ERR_INVALID, "page beyond the arena");
     char* kd = reinterpret_cast<char*>(kv->k[layer]) + pages[i] * pb;
     char* vd = reinterpret_cast<char*>(kv->v[layer]) + pages[i] * pb;
-    if (read) {
+    if (kv->f32) {  // K in V's layout: plain copies
+      if (read) {
+        if (k) YX_HIP(hipMemcpyAsync(static_cast<char*>(k) + i * pb, kd, pb, hipMemcpyDeviceToHost, c->stream));
+        if (v) YX_HIP(hipMemcpyAsync(static_cast<char*>(v) + i * pb, vd, pb, hipMemcpyDeviceToHost, c->stream));
+      } else {
+        if (k) YX_HIP(hipMemcpyAsync(kd, static_cast<const char*>(k) + i * pb, pb, hipMemcpyHostToDevice, c->stream));
+        if (v) YX_HIP(hipMemcpyAsync(vd, static_cast<const char*>(v) + i * pb, pb, hipMemcpyHostToDevice, c->stream));
+      }
+    } else if (read) {
       if (k) {
         YX_HIP(hipMemcpyAsync(tmp.data(), kd, pb, hipMemcpyDeviceToHost, c->stream));
         YX_HIP(hipStreamSynchronize(c->stream));
