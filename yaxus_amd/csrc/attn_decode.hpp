@@ -10,10 +10,13 @@
 //
 // Work item = (a group of consecutive rows of one sequence, one KV head, one chunk of
 // 16-key blocks), one workgroup of W waves; the waves split the chunk's blocks and
-// merge through LDS. The group's (row, query head) pairs are "logical rows"; NT tiles
-// of 8 logical rows each sit in MFMA columns as an f16 hi part (columns 0-7) and an
-// f16 lo part (columns 8-15) of q, so q.k keeps ~2^-22 relative accuracy with f16 K
-// exact and f32 accumulation. Per block of 16 keys:
+// merge through LDS. The group's (row, query head) pairs are "logical rows". Three
+// kernels below: the 8-row-tile kernels (`paged_attn_decode`, and the queue-balanced
+// one-tile `paged_attn_decode_balanced`) and the 16-row-tile one
+// (`paged_attn_decode_wide`), plus the f32-arena kernel at the end. In the 8-row
+// tiles, NT tiles of 8 logical rows each sit in MFMA columns as an f16 hi part
+// (columns 0-7) and an f16 lo part (columns 8-15) of q, so q.k keeps ~2^-22 relative
+// accuracy with f16 K exact and f32 accumulation. Per block of 16 keys:
 //   S^T[key][col] = K[key][:] . Q[col][:]         4 x v_mfma_f32_16x16x32_f16
 //   online softmax per column; P = exp2(S*scale*log2e - m) split into hi/lo f16
 //   O^T[dim][col] += V^T[dim][key] P^T[key][col]  8 x v_mfma_f32_16x16x32_f16 per 2 blocks
@@ -825,8 +828,10 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
   });
 }
 
-// Wide multi-tile decode (verify passes and groups of 9-32 logical rows): tiles of 16
-// logical rows, one per MFMA column. q's f16 hi and lo parts are two B operands whose
+// 16-row-tile decode (NT = 1 or 2 tiles of 16 logical rows): the kernel for passes of
+// more than 8 logical rows per work item (verify), and for one-tile passes whose work
+// items split evenly over its waves or are longer than the queue kernel takes. Each
+// logical row is one MFMA column: q's f16 hi and lo parts are two B operands whose
 // products accumulate into the same S (and P's into the same O), instead of taking two
 // columns per row as in the 8-row tiles: the same MFMA work per logical row, half the
 // softmax arithmetic (no column is duplicated), and, with one-block register sets, a
