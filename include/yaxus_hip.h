@@ -60,9 +60,12 @@ int yx_sync(yx_ctx* ctx);
  * so do one-tile passes whose work items split evenly over the waves or hold more than
  * 64 blocks; other one-tile passes use the kernel whose waves share a queue of blocks.
  * 1: the kernels with 8-row tiles and a fixed split only. 2: the 16-row-tile kernel for
- * every decode pass). Setting an option drops
- * cached work lists. Values are positive; 0 is accepted for attn_target_waves and
- * attn_decode_shape. */
+ * every decode pass). "attn_cascade" (1, the default: consecutive groups of a one-tile
+ * decode pass whose page tables start with the same pages, e.g. forks of one prompt,
+ * attend those shared keys once for all their rows and merge that result into each
+ * row's own; 0: every group reads its whole context). Setting an option drops
+ * cached work lists. Values are positive; 0 is accepted for attn_target_waves,
+ * attn_decode_shape and attn_cascade. */
 int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
 
 /* Backend::new_kv (lib.rs:118; GPU ops/mod.rs:42-66): `layers` layers of `pages`

@@ -53,7 +53,25 @@ struct AttnItem {
   uint32_t nch;        // chunks of the group (at most kMaxChunks)
   uint32_t part_base;  // first partial slot of the group
   uint32_t counter;    // arrival counter index of the group
-  uint32_t pad[3];
+  // Shared-prefix (cascade) passes. A prefix item (pref_info has kPrefixItem) attends
+  // keys that every row of a run of consecutive groups shares (the same pages) for all
+  // of their rows at once: pref_base / pref_nch then index its member groups in the
+  // member list. A member group's items carry pref_base / pref_nch = the first partial
+  // slot and chunk count of its prefix items and pref_info = the group's first row's
+  // offset within them; its merge takes the prefix chunks first, then its own.
+  uint32_t pref_base;
+  uint32_t pref_nch;   // 0: no shared prefix
+  uint32_t pref_info;
+};
+static constexpr uint32_t kPrefixItem = 0x80000000u;
+
+// A member group of a shared prefix, for the prefix items' hand-off.
+struct SubRef {
+  uint32_t r0, nrows;      // the group's rows
+  uint32_t part_base, nch;  // its own chunks' partial slots
+  uint32_t counter;         // its arrival counter
+  uint32_t row_off;         // its first row's offset among the prefix items' rows
+  uint32_t pad[2];
 };
 
 static constexpr float kLog2e = 1.4426950408889634f;
@@ -187,58 +205,29 @@ __device__ __forceinline__ void fused_append(const AttnItem& it, uint32_t kh, ui
   __syncthreads();
 }
 
-// Hands a workgroup's result for its logical rows on: straight to `out` when the item
-// is its group's only chunk, else to the item's partial slot, after which the last item
-// of the group to arrive merges all partials in chunk order (so the result does not
-// depend on arrival order). value(lr, qi, mt, lt, o) gives the workgroup's maximum, sum
-// and unnormalised O (dims 4qi..4qi+3) of logical row lr.
-template <int kThreads, int kRows, typename Value>
-__device__ __forceinline__ void finish_item(const AttnItem& it, uint32_t kh, uint32_t G, uint32_t hq,
-                                            uint32_t hkv, uint32_t nlog, float* __restrict__ out,
-                                            float* __restrict__ part_o, float2* __restrict__ part_ml,
-                                            uint32_t* __restrict__ counters, uint32_t part_o_bytes,
-                                            uint32_t part_ml_bytes, uint32_t& last, Value value) {
-  const size_t qd = static_cast<size_t>(hq) * kD;
-  const uint32_t rows_per_slot = kRows;
-  const size_t slot = (static_cast<size_t>(it.part_base) + it.chunk) * hkv + kh;
-  const __amdgpu_buffer_rsrc_t ro = make_rsrc(part_o, part_o_bytes);
-  const __amdgpu_buffer_rsrc_t rml = make_rsrc(part_ml, part_ml_bytes);
+// Merges one group of a split-K pass (the last arrival does it): its chunk list is npre
+// prefix chunks (slots from pre_base, logical rows from row_off * G on) followed by its
+// own nown chunks (slots from own_base). A thread merges one (row, 4 dims) over a range
+// of the list in list order, with a running maximum; the loads of 8 chunks are in
+// flight at a time. With more than one round of loads (over 8 chunks) and threads to
+// spare, the list is cut into `parts` contiguous ranges, each merged by its own
+// nlog * 32 threads; part 0 then adds the others' results in part order through LDS (a
+// fixed order, so the result does not depend on timing).
+template <int kThreads, int kRows>
+__device__ __forceinline__ void merge_group(uint32_t g_r0, uint32_t g_nrows, uint32_t own_base,
+                                         uint32_t nown, uint32_t pre_base, uint32_t npre,
+                                         uint32_t row_off, uint32_t kh, uint32_t G, uint32_t hq,
+                                         uint32_t hkv, float* __restrict__ out,
+                                         __amdgpu_buffer_rsrc_t ro, __amdgpu_buffer_rsrc_t rml) {
+  __shared__ float4 part_o_lds[kThreads];
+  __shared__ float2 part_ml_lds[kThreads];
   constexpr int kPer = (kRows * 32 + kThreads - 1) / kThreads;
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const uint32_t idx = threadIdx.x + k * kThreads;
-    const uint32_t lr = idx >> 5, qi = idx & 31;
-    if (lr >= nlog || lr >= kRows) continue;
-    float mt, lt;
-    float4 o;
-    value(lr, qi, mt, lt, o);
-    if (it.nch == 1) {
-      const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
-      const float inv = 1.0f / lt;
-      *reinterpret_cast<float4*>(out + rr * qd + h * kD + qi * 4) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
-    } else {
-      const size_t e = slot * rows_per_slot + lr;
-      st4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4), o);
-      if (qi == 0) st2_coherent(rml, static_cast<uint32_t>(e * 8), float2{mt, lt});
-    }
-  }
-  if (it.nch == 1) return;
-
-  // The last work item of this (group, kv head) to arrive merges all of them.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  uint32_t* cnt = counters + static_cast<size_t>(it.counter) * hkv + kh;
-  if (threadIdx.x == 0) {
-    const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = arrived == it.nch - 1;
-    if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!last) return;
-
-  // A thread merges one (row, 4 dims) over a range of chunks in chunk order, with a
-  // running maximum; the loads of 8 chunks are in flight at a time.
-  const size_t base0 = static_cast<size_t>(it.part_base) * hkv + kh;
+  const size_t qd = static_cast<size_t>(hq) * kD;
+  const uint32_t g_nlog = g_nrows * G, nall = npre + nown;
+  auto entry = [&](uint32_t j, uint32_t lr) -> size_t {
+    return j < npre ? ((static_cast<size_t>(pre_base) + j) * hkv + kh) * kRows + row_off * G + lr
+                    : ((static_cast<size_t>(own_base) + (j - npre)) * hkv + kh) * kRows + lr;
+  };
   auto merge_range = [&](uint32_t lr, uint32_t qi, uint32_t c_begin, uint32_t c_end, float& mt,
                          float& lt, float4& o) {
     for (uint32_t c0 = c_begin; c0 < c_end; c0 += 8) {
@@ -246,8 +235,7 @@ __device__ __forceinline__ void finish_item(const AttnItem& it, uint32_t kh, uin
       float4 po[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const uint32_t ch = min(c0 + j, c_end - 1);
-        const size_t e = (base0 + static_cast<size_t>(ch) * hkv) * rows_per_slot + lr;
+        const size_t e = entry(min(c0 + j, c_end - 1), lr);
         ml[j] = ld2_coherent(rml, static_cast<uint32_t>(e * 8));
         po[j] = ld4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4));
       }
@@ -266,53 +254,132 @@ __device__ __forceinline__ void finish_item(const AttnItem& it, uint32_t kh, uin
     }
   };
   auto store_row = [&](uint32_t lr, uint32_t qi, float lt, const float4& o) {
-    const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
+    const uint32_t rr = g_r0 + lr / G, h = kh * G + lr % G;
     const float inv = 1.0f / lt;
     *reinterpret_cast<float4*>(out + rr * qd + h * kD + qi * 4) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
   };
-  // With more than one round of loads (over 8 chunks) and threads to spare, the chunk
-  // list is cut into `parts` contiguous ranges, each merged by its own nlog * 32
-  // threads; part 0 then adds the others' results in part order through LDS (a fixed
-  // order, so the result does not depend on timing).
-  const uint32_t span = nlog * 32;
-  const uint32_t parts = min(static_cast<uint32_t>(kThreads) / span, (it.nch + 7) / 8);  // uniform
+  const uint32_t span = g_nlog * 32;
+  const uint32_t parts = min(static_cast<uint32_t>(kThreads) / span, (nall + 7) / 8);  // uniform
   if (parts >= 2) {
-    __shared__ float4 part_o_lds[kThreads];
-    __shared__ float2 part_ml_lds[kThreads];
     const uint32_t part = threadIdx.x / span, pi = threadIdx.x - part * span;
     const uint32_t lr = pi >> 5, qi = pi & 31;
     float mt = -INFINITY, lt = 0.0f;
     float4 o = {0, 0, 0, 0};
-    if (part < parts) merge_range(lr, qi, it.nch * part / parts, it.nch * (part + 1) / parts, mt, lt, o);
+    if (part < parts) merge_range(lr, qi, nall * part / parts, nall * (part + 1) / parts, mt, lt, o);
     if (part > 0 && part < parts) {
       part_o_lds[threadIdx.x] = o;
       part_ml_lds[threadIdx.x] = float2{mt, lt};
     }
     __syncthreads();
-    if (part != 0) return;
-    for (uint32_t pp = 1; pp < parts; ++pp) {
-      const float2 b = part_ml_lds[pp * span + pi];
-      if (!(b.y > 0.0f)) continue;
-      const float4 ob = part_o_lds[pp * span + pi];
-      const float mn = fmaxf(mt, b.x);
-      const float r = __builtin_amdgcn_exp2f(mt - mn), wt = __builtin_amdgcn_exp2f(b.x - mn);
-      lt = lt * r + b.y * wt;
-      o = float4{o.x * r + ob.x * wt, o.y * r + ob.y * wt, o.z * r + ob.z * wt, o.w * r + ob.w * wt};
-      mt = mn;
+    if (part == 0) {
+      for (uint32_t pp = 1; pp < parts; ++pp) {
+        const float2 b = part_ml_lds[pp * span + pi];
+        if (!(b.y > 0.0f)) continue;
+        const float4 ob = part_o_lds[pp * span + pi];
+        const float mn = fmaxf(mt, b.x);
+        const float r = __builtin_amdgcn_exp2f(mt - mn), wt = __builtin_amdgcn_exp2f(b.x - mn);
+        lt = lt * r + b.y * wt;
+        o = float4{o.x * r + ob.x * wt, o.y * r + ob.y * wt, o.z * r + ob.z * wt, o.w * r + ob.w * wt};
+        mt = mn;
+      }
+      store_row(lr, qi, lt, o);
     }
-    store_row(lr, qi, lt, o);
+    __syncthreads();  // the LDS results are read before another merge reuses them
     return;
   }
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const uint32_t idx = threadIdx.x + k * kThreads;
     const uint32_t lr = idx >> 5, qi = idx & 31;
-    if (lr >= nlog || lr >= kRows) continue;
+    if (lr >= g_nlog || lr >= kRows) continue;
     float mt = -INFINITY, lt = 0.0f;
     float4 o = {0, 0, 0, 0};
-    merge_range(lr, qi, 0, it.nch, mt, lt, o);
+    merge_range(lr, qi, 0, nall, mt, lt, o);
     store_row(lr, qi, lt, o);
   }
+}
+
+// Hands a workgroup's result for its logical rows on: straight to `out` when the item
+// is its group's only chunk, else to the item's partial slot, after which the last item
+// of the group to arrive merges all partials in chunk order (so the result does not
+// depend on arrival order). value(lr, qi, mt, lt, o) gives the workgroup's maximum, sum
+// and unnormalised O (dims 4qi..4qi+3) of logical row lr. With a shared prefix the
+// group's chunk list is the prefix items' chunks, then its own; a prefix item arrives at
+// every member group and merges each one it completes.
+template <int kThreads, int kRows, bool kCascade = false, typename Value>
+__device__ __forceinline__ void finish_item(const AttnItem& it, uint32_t kh, uint32_t G, uint32_t hq,
+                                            uint32_t hkv, uint32_t nlog, float* __restrict__ out,
+                                            float* __restrict__ part_o, float2* __restrict__ part_ml,
+                                            uint32_t* __restrict__ counters, uint32_t part_o_bytes,
+                                            uint32_t part_ml_bytes, uint32_t& last, Value value,
+                                            const SubRef* __restrict__ members = nullptr) {
+  const size_t qd = static_cast<size_t>(hq) * kD;
+  const uint32_t rows_per_slot = kRows;
+  const bool is_prefix = kCascade && (it.pref_info & kPrefixItem) != 0;
+  const uint32_t total = it.nch + (kCascade && !is_prefix ? it.pref_nch : 0u);  // chunks of the group
+  const bool direct = !is_prefix && total == 1;
+  const size_t slot = (static_cast<size_t>(it.part_base) + it.chunk) * hkv + kh;
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(part_o, part_o_bytes);
+  const __amdgpu_buffer_rsrc_t rml = make_rsrc(part_ml, part_ml_bytes);
+  constexpr int kPer = (kRows * 32 + kThreads - 1) / kThreads;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t idx = threadIdx.x + k * kThreads;
+    const uint32_t lr = idx >> 5, qi = idx & 31;
+    if (lr >= nlog || lr >= kRows) continue;
+    float mt, lt;
+    float4 o;
+    value(lr, qi, mt, lt, o);
+    if (direct) {
+      const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
+      const float inv = 1.0f / lt;
+      *reinterpret_cast<float4*>(out + rr * qd + h * kD + qi * 4) = float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+    } else {
+      const size_t e = slot * rows_per_slot + lr;
+      st4_coherent(ro, static_cast<uint32_t>((e * kD + qi * 4) * 4), o);
+      if (qi == 0) st2_coherent(rml, static_cast<uint32_t>(e * 8), float2{mt, lt});
+    }
+  }
+  if (direct) return;
+
+  // Arrival: at the item's own group, or (prefix item) at every member group; a group's
+  // last arrival merges it.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if constexpr (kCascade) {
+    if (is_prefix) {
+      __shared__ uint32_t done[16];  // the member groups this item completes
+      const uint32_t nm = it.pref_nch;
+      if (threadIdx.x < nm) {
+        const SubRef& sr = members[it.pref_base + threadIdx.x];
+        uint32_t* cnt = counters + static_cast<size_t>(sr.counter) * hkv + kh;
+        const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool fin = arrived == sr.nch + it.nch - 1;
+        if (fin) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        done[threadIdx.x] = fin;
+      }
+      __syncthreads();
+      for (uint32_t m = 0; m < nm; ++m) {
+        if (!done[m]) continue;  // uniform (LDS)
+        const SubRef sr = members[it.pref_base + m];
+        merge_group<kThreads, kRows>(sr.r0, sr.nrows, sr.part_base, sr.nch, it.part_base, it.nch,
+                                     sr.row_off, kh, G, hq, hkv, out, ro, rml);
+      }
+      return;
+    }
+  }
+  if (threadIdx.x == 0) {
+    uint32_t* cnt = counters + static_cast<size_t>(it.counter) * hkv + kh;
+    const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = arrived == total - 1;
+    if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+
+  if (!last) return;
+  merge_group<kThreads, kRows>(it.r0, it.nrows, it.part_base, it.nch,
+                               kCascade ? it.pref_base : 0u, kCascade ? it.pref_nch : 0u,
+                               kCascade ? it.pref_info : 0u, kh, G, hq, hkv, out, ro, rml);
 }
 
 template <int NT, int kWaves = DecodeWaves<NT>::value>
@@ -335,7 +402,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_attn_decode(
   const uint32_t G = hq / hkv;
   const uint32_t nlog = it.nrows * G;  // logical rows in the group
 
-  if (knew != nullptr && it.chunk == it.nch - 1)
+  if (knew != nullptr && it.chunk == it.nch - 1 && !(it.pref_info & kPrefixItem))
     fused_append<64 * kWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
 
   // This wave's share of the item's blocks, [wb0, wb1), in whole quads of blocks (a
@@ -601,7 +668,7 @@ __device__ __forceinline__ void fused_write_rows(const AttnItem& it, uint32_t kh
                                                  const QkvIn& qi_in, float (*q_lds)[kD],
                                                  float* qsq, int wave, int lane, _Float16* kw,
                                                  _Float16* vw) {
-  const uint32_t nk = it.chunk == it.nch - 1 ? it.nrows : 0;
+  const uint32_t nk = (it.chunk == it.nch - 1 && !(it.pref_info & kPrefixItem)) ? it.nrows : 0;
   const uint32_t qd = hq * kD, kvd = hkv * kD, cols = qd + 2 * kvd;
   for (uint32_t t = static_cast<uint32_t>(wave); t < nlog + nk; t += kWaves) {
     float o0, o1;
@@ -653,7 +720,7 @@ __global__ __launch_bounds__(64 * kBalWaves) void paged_attn_decode_balanced(
   if constexpr (QKV) {
     fused_write_rows<kBalWaves>(it, kh, G, hq, hkv, nlog, bpp_shift, pos, kv_slot, qi_in, sh.q,
                                 sh.qsq[wave], wave, lane, kw, vw);
-  } else if (knew != nullptr && it.chunk == it.nch - 1) {
+  } else if (knew != nullptr && it.chunk == it.nch - 1 && !(it.pref_info & kPrefixItem)) {
     fused_append<64 * kBalWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
   } else {
     __syncthreads();
@@ -863,7 +930,8 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
     const float* __restrict__ knew, const float* __restrict__ vnew,
     const uint32_t* __restrict__ kv_slot, _Float16* kw, _Float16* vw,  // kw/vw alias kc/vc
     uint32_t part_o_bytes, uint32_t part_ml_bytes, uint32_t hq, uint32_t hkv,
-    uint32_t bpp_shift, uint32_t window, float scale_log2, QkvIn qi_in) {
+    uint32_t bpp_shift, uint32_t window, float scale_log2, QkvIn qi_in,
+    const SubRef* __restrict__ members) {
   static_assert(!QKV || NT == 1, "write_rows is fused for one tile only (LDS)");
   __shared__ WideShared<NT, QKV> sh;
   const AttnItem it = items[blockIdx.x];
@@ -877,7 +945,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
   if constexpr (QKV)
     fused_write_rows<kWideWaves>(it, kh, G, hq, hkv, nlog, bpp_shift, pos, kv_slot, qi_in, sh.q,
                                  sh.qsq[wave], wave, lane, kw, vw);
-  else if (knew != nullptr && it.chunk == it.nch - 1)
+  else if (knew != nullptr && it.chunk == it.nch - 1 && !(it.pref_info & kPrefixItem))
     fused_append<64 * kWideWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
 
   // This wave's share of the item's blocks, [wb0, wb1): shares differ by at most one
@@ -1036,7 +1104,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
   }
   __syncthreads();
 
-  finish_item<64 * kWideWaves, NT * 16>(it, kh, G, hq, hkv, nlog, out, part_o, part_ml, counters,
+  finish_item<64 * kWideWaves, NT * 16, true>(it, kh, G, hq, hkv, nlog, out, part_o, part_ml, counters,
                                         part_o_bytes, part_ml_bytes, sh.last,
                                         [&](uint32_t lr, uint32_t qi, float& mt, float& lt, float4& o) {
     mt = -INFINITY;
@@ -1055,7 +1123,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
       o.z += ow.z * wt;
       o.w += ow.w * wt;
     }
-  });
+  }, members);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1125,7 +1193,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_f32(
     const float* __restrict__ knew, const float* __restrict__ vnew,
     const uint32_t* __restrict__ kv_slot, float* kw, float* vw,  // kw/vw alias kc/vc
     uint32_t part_o_bytes, uint32_t part_ml_bytes, uint32_t hq, uint32_t hkv,
-    uint32_t bpp_shift, uint32_t window, float scale_log2) {
+    uint32_t bpp_shift, uint32_t window, float scale_log2, const SubRef* __restrict__ members) {
   __shared__ WideShared<1, false> sh;
   const AttnItem it = items[blockIdx.x];
   const uint32_t kh = blockIdx.y;
@@ -1135,7 +1203,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_f32(
   const uint32_t G = hq / hkv;
   const uint32_t nlog = it.nrows * G;  // logical rows in the group (at most 16)
 
-  if (knew != nullptr && it.chunk == it.nch - 1)
+  if (knew != nullptr && it.chunk == it.nch - 1 && !(it.pref_info & kPrefixItem))
     fused_append_f32<64 * kWideWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
 
   const uint32_t nall = it.blk1 - it.blk0;
@@ -1252,7 +1320,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_f32(
   }
   __syncthreads();
 
-  finish_item<64 * kWideWaves, 16>(it, kh, G, hq, hkv, nlog, out, part_o, part_ml, counters,
+  finish_item<64 * kWideWaves, 16, true>(it, kh, G, hq, hkv, nlog, out, part_o, part_ml, counters,
                                    part_o_bytes, part_ml_bytes, sh.last,
                                    [&](uint32_t lr2, uint32_t qi, float& mt, float& lt, float4& o) {
     mt = -INFINITY;
@@ -1271,7 +1339,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_f32(
       o.z += ow.z * wt;
       o.w += ow.w * wt;
     }
-  });
+  }, members);
 }
 
 }  // namespace yx

@@ -120,6 +120,9 @@ struct AttnPlan {
   bool f32 = false;   // the f32-arena kernel
   std::vector<yx::AttnItem> items;
   DevBuf d_items;
+  std::vector<yx::SubRef> members;  // member groups of shared prefixes
+  DevBuf d_members;
+  size_t cascades = 0;              // shared prefixes attended once for their groups
   bool fusable = false;  // the append can run inside the attention kernel
   size_t slots = 0;     // partial slots (per kv head)
   size_t counters = 0;  // arrival counters (per kv head)
@@ -171,7 +174,7 @@ struct yx_ctx {
   uint32_t max_page = 0, max_slot = 0;
   DevBuf d_pos, d_slot, d_pages;
   bool have_pass = false;
-  std::map<std::tuple<size_t, size_t, size_t, bool>, AttnPlan> plans;  // (window, hq, hkv, f32)
+  std::map<std::tuple<size_t, size_t, size_t, bool, size_t>, AttnPlan> plans;  // (window, hq, hkv, f32, page)
   // scratch
   DevBuf part_o, part_ml, counters, io_a, io_b, io_c, io_q;
   // options
@@ -186,6 +189,7 @@ struct yx_ctx {
   // 0: automatic (the queue or the 16-row-tile kernel), 1: 8-row-tile static split only,
   // 2: the 16-row-tile kernel for every decode pass.
   long decode_shape = 0;
+  long cascade = 1;  // attend keys shared by consecutive groups (same pages) once for all of them
   bool profiling = false;
   Profile prof[4];
   bool capturing = false;
@@ -249,8 +253,10 @@ static constexpr uint32_t kFanIn = 32;  // chunks per group the automatic split 
 
 // f32: the plan of the f32-arena kernel (split-K decode for every pass, 16 logical rows
 // per work item).
-int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, AttnPlan** out) {
-  auto key = std::make_tuple(window, hq, hkv, f32);
+// page_size: the arena's (shared prefixes are found by page ids).
+int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t page_size,
+               AttnPlan** out) {
+  auto key = std::make_tuple(window, hq, hkv, f32, page_size);
   auto it = c->plans.find(key);
   if (it != c->plans.end()) {
     *out = &it->second;
@@ -308,6 +314,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, AttnPl
 
   struct Sub {
     uint32_t r0, n, pt_off, b0, b1;
+    int casc = -1;  // the shared prefix it belongs to
   };
   std::vector<Sub> subs;
   size_t work = 0;
@@ -330,6 +337,56 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, AttnPl
       subs.push_back(s);
     }
   }
+  // Shared prefixes (cascade attention): a run of consecutive groups in consecutive pass
+  // rows whose page tables start with the same pages reads those keys once, as one
+  // group of all their rows (at most 16 logical rows, one tile of the 16-row-tile
+  // kernel), instead of once per group. Only keys every row of the run sees (below
+  // each row's position, no window cut) are shared; at least kMinShared blocks.
+  struct Casc {
+    uint32_t r0, n, pt_off, blocks, first, count;
+  };
+  std::vector<Casc> cascs;
+  const uint32_t bpp = static_cast<uint32_t>(page_size / 16);  // blocks per page
+  constexpr uint32_t kMinShared = 16;
+  if (c->cascade && nt == 1 && c->decode_shape == 0) {
+    const uint32_t cap_rows = static_cast<uint32_t>(16 / G);
+    for (size_t i = 0; i < subs.size();) {
+      size_t j = i + 1;
+      uint32_t rows = subs[i].n;
+      const uint32_t first_page = c->pages[subs[i].pt_off];
+      while (j < subs.size() && subs[j].r0 == subs[j - 1].r0 + subs[j - 1].n &&
+             rows + subs[j].n <= cap_rows && subs[j].b0 == 0 && subs[i].b0 == 0 &&
+             c->pages[subs[j].pt_off] == first_page)
+        rows += subs[j++].n;
+      if (j - i >= 2) {
+        // Blocks every row sees: below the smallest position's block (so the rows' own
+        // new keys are never in the shared part) and within the common pages.
+        uint32_t blocks = UINT32_MAX;
+        for (size_t k = i; k < j; ++k)
+          for (uint32_t r = subs[k].r0; r < subs[k].r0 + subs[k].n; ++r)
+            blocks = std::min(blocks, c->pos[r] / 16);
+        uint32_t pages_common = (blocks + bpp - 1) / bpp;
+        for (size_t k = i + 1; k < j; ++k) {
+          uint32_t p = 0;
+          while (p < pages_common && c->pages[subs[k].pt_off + p] == c->pages[subs[i].pt_off + p]) ++p;
+          pages_common = p;
+        }
+        blocks = std::min(blocks, pages_common * bpp);
+        if (blocks >= kMinShared) {
+          Casc cc{subs[i].r0, rows, subs[i].pt_off, blocks, static_cast<uint32_t>(i),
+                  static_cast<uint32_t>(j - i)};
+          for (size_t k = i; k < j; ++k) {
+            work -= blocks;  // read once below, not once per group
+            subs[k].b0 = blocks;
+            subs[k].casc = static_cast<int>(cascs.size());
+          }
+          work += blocks;
+          cascs.push_back(cc);
+        }
+      }
+      i = j;
+    }
+  }
   work *= hkv;
   // Work items (workgroups of DecodeWaves waves) aimed at: target_waves / waves.
   // One workgroup per CU runs at a time for every tile count (8 waves of ~220
@@ -346,25 +403,94 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, AttnPl
   // items take 2-block units): with less, waves of every work item sit idle and the
   // extra chunks only lengthen the merge (small passes, e.g. sliding windows).
   if (c->target_waves == 0) cb = std::max<size_t>(cb, (nt == 1 ? 2 : 4) * waves);
+  // Quads per chunk of a group of nq quads for chunks of about cb blocks: at most
+  // kMaxChunks chunks, and (automatic split) at most kFanIn chunks per group while
+  // chunks stay within the one-tile queue kernel's 16 quads: a few long sequences
+  // would otherwise be cut into many short chunks (2 blocks per wave) whose merge
+  // outweighs the parallelism (B=1, ctx 16384: 64 chunks of 16 blocks 21.9 us, 32 of
+  // 32 blocks 17.3 us).
+  auto chunk_quads = [&](uint32_t nq, size_t cbk) {
+    uint32_t cq = static_cast<uint32_t>(std::max<size_t>((cbk + 3) / 4, (nq + yx::kMaxChunks - 1) / yx::kMaxChunks));
+    if (c->target_waves == 0) cq = std::max(cq, std::min<uint32_t>(yx::kBalQuads, (nq + kFanIn - 1) / kFanIn));
+    return cq;
+  };
+  // Whether every chunk's blocks split evenly over kWideWaves waves.
+  auto exact_split = [&](size_t cbk) {
+    auto check = [&](uint32_t nblocks) {
+      const uint32_t nq = (nblocks + 3) / 4, cq = chunk_quads(nq, cbk), nch = (nq + cq - 1) / cq;
+      for (uint32_t ch = 0; ch < nch; ++ch) {
+        const uint32_t b0 = 4 * static_cast<uint32_t>(static_cast<uint64_t>(nq) * ch / nch);
+        const uint32_t b1 = std::min(nblocks, 4 * static_cast<uint32_t>(static_cast<uint64_t>(nq) * (ch + 1) / nch));
+        if ((b1 - b0) % yx::kWideWaves != 0) return false;
+      }
+      return true;
+    };
+    for (const Sub& sb : subs)
+      if (!check(sb.b1 - sb.b0)) return false;
+    for (const Casc& cc : cascs)
+      if (!check(cc.blocks)) return false;
+    return true;
+  };
+  // Mid-size passes whose split is not exact anyway: work items of at least
+  // kMinItemBlocks blocks (six per wave) while that still gives work to more than half
+  // the CUs; shorter items spend more of their time in the start and the split-K
+  // hand-off than they save in parallelism (cfg2, 8.2k blocks: 33-block items 22.0 us,
+  // 52-block items 19.1; B=6 ctx 4096: 20.6 -> 15.5). Exact splits (the headline; B=8,
+  // ctx 4096) and small passes keep one item per CU.
+  constexpr size_t kMinItemBlocks = 48;
+  if (c->target_waves == 0 && nt == 1 && work >= static_cast<size_t>(c->cus) * kMinItemBlocks / 2 &&
+      !exact_split(cb))
+    cb = std::max<size_t>(cb, kMinItemBlocks);
   // Each wave's page ids fit its 64 lanes: at most 64 blocks per wave.
   cb = std::max<size_t>(1, std::min<size_t>({cb, static_cast<size_t>(c->max_chunk_blocks), 64 * waves}));
 
   AttnPlan plan;
   plan.nt = static_cast<int>(nt);
-  plan.wide = wide;
+  plan.wide = wide || !cascs.empty();
   size_t slot = 0;
+  // The shared prefixes' items first (they are the longest-lived inputs of their
+  // groups' merges); their partial slots always exist.
+  std::vector<uint32_t> casc_base(cascs.size()), casc_nch(cascs.size()), casc_moff(cascs.size());
+  for (size_t ci = 0; ci < cascs.size(); ++ci) {
+    const Casc& cc = cascs[ci];
+    const uint32_t nq = (cc.blocks + 3) / 4;
+    const uint32_t cq = chunk_quads(nq, cb);
+    const uint32_t nch = (nq + cq - 1) / cq;
+    casc_base[ci] = static_cast<uint32_t>(slot);
+    casc_nch[ci] = nch;
+    const uint32_t moff = static_cast<uint32_t>(plan.members.size());
+    casc_moff[ci] = moff;
+    for (uint32_t k = cc.first; k < cc.first + cc.count; ++k) {
+      yx::SubRef m{};
+      m.r0 = subs[k].r0;
+      m.nrows = subs[k].n;
+      m.counter = k;
+      m.row_off = subs[k].r0 - cc.r0;
+      plan.members.push_back(m);  // part_base and nch are set with the group's items
+    }
+    for (uint32_t ch = 0; ch < nch; ++ch) {
+      yx::AttnItem w{};
+      w.r0 = cc.r0;
+      w.nrows = cc.n;
+      w.pt_off = cc.pt_off;
+      w.blk0 = 4 * static_cast<uint32_t>(static_cast<uint64_t>(nq) * ch / nch);
+      w.blk1 = std::min(cc.blocks, 4 * static_cast<uint32_t>(static_cast<uint64_t>(nq) * (ch + 1) / nch));
+      w.chunk = ch;
+      w.nch = nch;
+      w.part_base = static_cast<uint32_t>(slot);
+      w.pref_base = moff;
+      w.pref_nch = cc.count;
+      w.pref_info = yx::kPrefixItem;
+      plan.items.push_back(w);
+    }
+    slot += nch;
+  }
   for (size_t si = 0; si < subs.size(); ++si) {
     const Sub& s = subs[si];
     // Chunks start on quads of blocks (the waves split them in quads), at most
     // kMaxChunks of them.
     const uint32_t nq = (s.b1 - s.b0 + 3) / 4;
-    uint32_t cq = static_cast<uint32_t>(std::max<size_t>((cb + 3) / 4, (nq + yx::kMaxChunks - 1) / yx::kMaxChunks));
-    // At most kFanIn chunks per group while chunks stay within the one-tile queue
-    // kernel's 16 quads: a few long sequences would otherwise be cut into many short
-    // chunks (2 blocks per wave) whose merge outweighs the parallelism (B=1, ctx 16384:
-    // 64 chunks of 16 blocks 21.9 us, 32 of 32 blocks 17.3 us).
-    if (c->target_waves == 0)
-      cq = std::max(cq, std::min<uint32_t>(yx::kBalQuads, (nq + kFanIn - 1) / kFanIn));
+    const uint32_t cq = chunk_quads(nq, cb);
     if (cq * 4 > 64 * waves)
       return fail(YX_ERR_UNSUPPORTED, "context too long for 256 chunks of the widest work item");
     const uint32_t nch = (nq + cq - 1) / cq;
@@ -379,9 +505,20 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, AttnPl
       w.nch = nch;
       w.part_base = static_cast<uint32_t>(slot);
       w.counter = static_cast<uint32_t>(si);
+      if (s.casc >= 0) {
+        w.pref_base = casc_base[s.casc];
+        w.pref_nch = casc_nch[s.casc];
+        w.pref_info = s.r0 - cascs[s.casc].r0;
+      }
       plan.items.push_back(w);
     }
-    if (nch > 1) slot += nch;
+    if (s.casc >= 0) {  // the prefix items' view of this group's own chunks
+      yx::SubRef& m = plan.members[casc_moff[s.casc] + (si - cascs[s.casc].first)];
+      m.part_base = static_cast<uint32_t>(slot);
+      m.nch = nch;
+    }
+    const uint32_t total = nch + (s.casc >= 0 ? casc_nch[s.casc] : 0);
+    if (total > 1) slot += nch;
   }
   // The fused append needs each group in one sub and the last chunk of each group to
   // hold all of its rows' keys (the first row's position is the smallest).
@@ -393,7 +530,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, AttnPl
       if (sb.n != c->groups[gi].n) plan.fusable = false;
     }
     for (const yx::AttnItem& w : plan.items) {
-      if (w.chunk + 1 != w.nch) continue;
+      if (w.chunk + 1 != w.nch || (w.pref_info & yx::kPrefixItem)) continue;
       uint32_t pmin = UINT32_MAX;
       for (uint32_t i = w.r0; i < w.r0 + w.nrows; ++i) pmin = std::min(pmin, c->pos[i]);
       if (w.blk0 * 16 > pmin) plan.fusable = false;
@@ -415,7 +552,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, AttnPl
     bool exact = true;
     for (const yx::AttnItem& w : plan.items)
       if ((w.blk1 - w.blk0) % yx::kWideWaves != 0) exact = false;
-    plan.wide = exact || !plan.balanced;
+    plan.wide = !cascs.empty() || exact || !plan.balanced;
   }
   plan.slots = slot;
   plan.counters = subs.size();
@@ -427,6 +564,13 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, AttnPl
   rc = c->staging[c->cur_staging].upload(p.d_items.p, p.items.data(),
                                          p.items.size() * sizeof(yx::AttnItem), c->stream);
   if (rc) return rc;
+  p.cascades = cascs.size();
+  if (!p.members.empty()) {
+    if ((rc = p.d_members.ensure(p.members.size() * sizeof(yx::SubRef), c->stream))) return rc;
+    rc = c->staging[c->cur_staging].upload(p.d_members.p, p.members.data(),
+                                           p.members.size() * sizeof(yx::SubRef), c->stream);
+    if (rc) return rc;
+  }
   *out = &p;
   return YX_OK;
 }
@@ -450,9 +594,9 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   if (c->rows == 0) return YX_OK;
   if (!out || (!q && !qkv)) return fail(YX_ERR_INVALID, "null q or out");
   AttnPlan* plan;
-  if (c->capturing && !c->plans.count(std::make_tuple(window, hq, hkv, kv->f32)))
+  if (c->capturing && !c->plans.count(std::make_tuple(window, hq, hkv, kv->f32, kv->page)))
     return fail(YX_ERR_INVALID, "run the call once before capturing it (its work list is uploaded then)");
-  if ((rc = build_plan(c, window, hq, hkv, kv->f32, &plan))) return rc;
+  if ((rc = build_plan(c, window, hq, hkv, kv->f32, kv->page, &plan))) return rc;
   // Logical rows per partial slot: the kernel's tile rows.
   const size_t rps = plan->wide ? static_cast<size_t>((plan->nt + 1) / 2) * 16 : static_cast<size_t>(plan->nt) * 8;
   if ((rc = c->part_o.ensure(std::max<size_t>(1, plan->slots * hkv * rps * 128 * 4), c->stream)))
@@ -517,6 +661,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   const uint32_t W = static_cast<uint32_t>(window);
   const uint32_t po_bytes = static_cast<uint32_t>(std::min<size_t>(c->part_o.cap, 0xffffffffu));
   const uint32_t pml_bytes = static_cast<uint32_t>(std::min<size_t>(c->part_ml.cap, 0xffffffffu));
+  const auto* mem = plan->members.empty() ? nullptr : static_cast<const yx::SubRef*>(plan->d_members.p);
 #define YX_LAUNCH_DECODE(NT)                                                                        \
   hipLaunchKernelGGL(yx::paged_attn_decode<NT>, grid, dim3(64 * yx::DecodeWaves<NT>::value), 0,      \
                      c->stream, items, pos, pages,                                                  \
@@ -527,7 +672,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     hipLaunchKernelGGL(yx::paged_attn_decode_f32, grid, dim3(64 * yx::kWideWaves), 0, c->stream,
                        items, pos, pages, kv->kf(layer), kv->vf(layer), q, out, po, pml, cnt, knew,
                        vnew, static_cast<const uint32_t*>(c->d_slot.p), kv->kf(layer),
-                       kv->vf(layer), po_bytes, pml_bytes, H, HK, P, W, scale_log2);
+                       kv->vf(layer), po_bytes, pml_bytes, H, HK, P, W, scale_log2, mem);
   } else if (plan->balanced && !plan->wide) {
 #define YX_LAUNCH_BAL(QKV, UB, KN, VN, IN)                                                          \
   hipLaunchKernelGGL((yx::paged_attn_decode_balanced<QKV, UB>), grid, dim3(64 * yx::kBalWaves), 0,  \
@@ -544,7 +689,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   hipLaunchKernelGGL((yx::paged_attn_decode_wide<NT, QKV>), grid, dim3(64 * yx::kWideWaves), 0,     \
                      c->stream, items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml,     \
                      cnt, KN, VN, static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer],        \
-                     kv->v[layer], po_bytes, pml_bytes, H, HK, P, W, scale_log2, IN)
+                     kv->v[layer], po_bytes, pml_bytes, H, HK, P, W, scale_log2, IN, mem)
     if (qkv) YX_LAUNCH_WIDE(1, true, nullptr, nullptr, *qkv);
     else if (plan->nt <= 2) YX_LAUNCH_WIDE(1, false, knew, vnew, yx::QkvIn{});
     else YX_LAUNCH_WIDE(2, false, knew, vnew, yx::QkvIn{});
@@ -670,7 +815,10 @@ int yx_ctx_destroy(yx_ctx* c) {
       (void)hipEventDestroy(e.first);
       (void)hipEventDestroy(e.second);
     }
-  for (auto& kv : c->plans) kv.second.d_items.release();
+  for (auto& kv : c->plans) {
+    kv.second.d_items.release();
+    kv.second.d_members.release();
+  }
   for (DevBuf* b : {&c->d_pos, &c->d_slot, &c->d_pages, &c->part_o, &c->part_ml, &c->counters,
                     &c->io_a, &c->io_b, &c->io_c, &c->io_q})
     b->release();
@@ -694,9 +842,10 @@ int yx_sync(yx_ctx* c) {
 int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
   if (!c || !key) return fail(YX_ERR_INVALID, "null argument");
   if (value < 0 || (value == 0 && std::strcmp(key, "attn_target_waves") &&
-                    std::strcmp(key, "attn_decode_shape")))
+                    std::strcmp(key, "attn_decode_shape") && std::strcmp(key, "attn_cascade")))
     return fail(YX_ERR_INVALID,
-                "option values are positive (attn_target_waves, attn_decode_shape: 0 = automatic)");
+                "option values are positive (attn_target_waves, attn_decode_shape: 0 = automatic; "
+                "attn_cascade: 0 = off)");
   if (!std::strcmp(key, "attn_target_waves"))
     c->target_waves = value;
   else if (!std::strcmp(key, "attn_max_tiles"))
@@ -707,10 +856,15 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
     c->prefill_min_rows = value;
   else if (!std::strcmp(key, "attn_max_chunk_blocks"))
     c->max_chunk_blocks = value;
+  else if (!std::strcmp(key, "attn_cascade"))
+    c->cascade = value ? 1 : 0;
   else
     return fail(YX_ERR_INVALID, std::string("unknown option ") + key);
   ++c->epoch;
-  for (auto& kv : c->plans) kv.second.d_items.release();
+  for (auto& kv : c->plans) {
+    kv.second.d_items.release();
+    kv.second.d_members.release();
+  }
   c->plans.clear();
   return YX_OK;
 }
@@ -912,7 +1066,10 @@ int yx_pass_begin(yx_ctx* c, size_t rows, const uint32_t* pos, const uint32_t* k
   if (rc) return rc;
   c->have_pass = false;
   ++c->epoch;
-  for (auto& kv : c->plans) kv.second.d_items.release();
+  for (auto& kv : c->plans) {
+    kv.second.d_items.release();
+    kv.second.d_members.release();
+  }
   c->plans.clear();
   c->rows = rows;
   c->npages = npages;
