@@ -53,7 +53,8 @@ int yx_sync(yx_ctx* ctx);
  * default, means one work item per CU), "attn_max_chunk_blocks" (most 16-key blocks per
  * work item), "attn_max_tiles" (most logical rows, in units of 8 (row, q head) pairs,
  * one decode work item holds, 1-4, default 4; 3 at most with attn_decode_shape 1 unless
- * one row's q heads need 4; a row's q heads always fit one work item),
+ * one row's q heads need 4, which then take the 16-row-tile kernel; a row's q heads
+ * always fit one work item),
  * "prefill_min_rows" (rows of one sequence from which the prefill kernel is used),
  * "attn_decode_shape" (0, the default: automatic. Passes of more than 8 logical rows per
  * work item use the kernel with 16-row tiles and a fixed split of blocks over its waves;

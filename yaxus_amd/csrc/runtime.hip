@@ -392,7 +392,9 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
   // One workgroup per CU runs at a time for every tile count (8 waves of ~220
   // registers, or 4 of more than 256), so by default the split aims at one work item
   // per CU: more would run in a second round.
-  const bool wide = f32 || (nt > 1 && c->decode_shape == 0) || c->decode_shape == 2;
+  // (Four 8-row tiles do not fit one wave's registers: a row with more than 24 q heads
+  // per KV head takes the 16-row-tile kernel whatever the shape option.)
+  const bool wide = f32 || (nt > 1 && c->decode_shape == 0) || c->decode_shape == 2 || nt > 3;
   const size_t waves = nt == 1 ? yx::DecodeWaves<1>::value
                                : (wide ? yx::kWideWaves : yx::DecodeWaves<2>::value);
   const size_t target_items = c->target_waves > 0
@@ -697,8 +699,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   } else switch (plan->nt) {
     case 1: YX_LAUNCH_DECODE(1); break;
     case 2: YX_LAUNCH_DECODE(2); break;
-    case 3: YX_LAUNCH_DECODE(3); break;
-    default: YX_LAUNCH_DECODE(4); break;  // only when one row has more than 24 q heads
+    default: YX_LAUNCH_DECODE(3); break;
   }
 #undef YX_LAUNCH_DECODE
   YX_HIP(hipGetLastError());
