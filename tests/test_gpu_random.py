@@ -46,3 +46,54 @@ def test_random_pass_matches_oracle(hip, seed):
             assert np.array_equal(kk[i], ok) and np.array_equal(vv[i], ov), f"{case}: page {p}"
     finally:
         sc.kv.destroy()
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_forked_pass_matches_oracle(hip, seed):
+    """Random forks of one or two prompts (shared whole pages, copied tails) mixed with
+    unrelated sequences, in random pass order: the shared-prefix path where it applies."""
+    rng = np.random.default_rng(7000 + seed)
+    hq, hkv = HEADS[rng.integers(len(HEADS))]
+    page = PAGES[rng.integers(4)]
+    prompts = [int(x) for x in rng.integers(page, 1400, int(rng.integers(1, 3)))]
+    nfork = [int(x) for x in rng.integers(2, 7, len(prompts))]
+    suffix = [[int(x) for x in rng.integers(0, 500, n)] for n in nfork]
+    loners = [int(x) for x in rng.integers(0, 900, int(rng.integers(0, 3)))]
+    rows = int(rng.choice([1, 1, 2]))
+    window = 0 if rng.integers(3) else int(rng.integers(200, 3000))
+    need = sum((p + page - 1) // page for p in prompts) + sum(
+        (p + s + rows + page - 1) // page + 1 for p, ss in zip(prompts, suffix) for s in ss) + sum(
+        (n + rows + page - 1) // page for n in loners)
+    sc = Scenario(hip, pages=need + 8, page=page, hkv=hkv, pool_seed=seed)
+    try:
+        seqs = []
+        for p, ss in zip(prompts, suffix):
+            base = sc.cache.new_seq()
+            sc.prefill({base: p})
+            for s in ss:
+                copies = []
+                f = sc.cache.fork(base, p, copies)
+                sc.hip.copy_pages(sc.kv, copies)
+                for c in copies:
+                    sc.orc[0].copy_page(c.src, c.dst)
+                if s:
+                    sc.prefill({f: s})
+                seqs.append(f)
+        for n in loners:
+            s = sc.cache.new_seq()
+            if n:
+                sc.prefill({s: n})
+            seqs.append(s)
+        order = [seqs[i] for i in rng.permutation(len(seqs))] if rng.integers(2) else seqs
+        pr = sc.run_pass([(s, rows) for s in order])
+        n = len(pr.meta.pos)
+        k = sc.draw(n * hkv * D).reshape(n, hkv, D)
+        v = sc.draw(n * hkv * D).reshape(n, hkv, D)
+        q = sc.draw(n * hq * D).reshape(n, hq * D)
+        got = sc.hip.attend_append(sc.kv, 0, k, v, q, hq, window=window)
+        sc.orc[0].store(pr.meta.kv_slot, k.reshape(n, -1), v.reshape(n, -1))
+        want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
+        case = f"heads {hq}/{hkv} page {page} prompts {prompts} suffix {suffix} rows {rows} window {window}"
+        assert close(got, want).all(), f"{case}: max abs err {np.abs(got - want).max()}"
+    finally:
+        sc.kv.destroy()
