@@ -628,6 +628,9 @@ struct BalancedShared {
   uint32_t last;
 };
 
+// kPolicy: the loads' cache policy (nontemporal for K/V read once; the default, which
+// keeps the lines in L2, for blocks that other work items read too).
+template <int kPolicy = kNontemporal>
 __device__ __forceinline__ void load_block_buf(BlockRegs& r, const _Float16* kblk, const _Float16* vblk,
                                                bool valid, int lane) {
   const int c = lane & 15, g = lane >> 4;
@@ -638,10 +641,10 @@ __device__ __forceinline__ void load_block_buf(BlockRegs& r, const _Float16* kbl
       __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(vblk), 0, bytes, 0x00020000);
 #pragma unroll
   for (int p = 0; p < 4; ++p)  // [p][key c][g] in 16-byte units
-    r.k[p] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, ((c * 4 + g) + p * 64) * 16, 0, kNontemporal));
+    r.k[p] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, ((c * 4 + g) + p * 64) * 16, 0, kPolicy));
 #pragma unroll
   for (int i = 0; i < 4; ++i)  // key 4g + i, dims c*8..c*8+7
-    r.v[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, ((4 * g + i) * kD + c * 8) * 2, 0, kNontemporal));
+    r.v[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, ((4 * g + i) * kD + c * 8) * 2, 0, kPolicy));
 }
 
 // The inputs of write_rows when the kernel runs it itself (Backend::attention in one
@@ -921,7 +924,11 @@ struct WideShared<NT, true> : WideShared<NT, false> {
 
 // QKV (one tile only): as in the queue kernel, the workgroup runs write_rows for its
 // rows first (queries into LDS, the last chunk's item stores the rows' K/V).
-template <int NT, bool QKV>
+// CASC: the pass has shared-prefix items, whose blocks other prefix items read as well:
+// those load with the default cache policy (kept in L2) instead of nontemporal (cfg2:
+// 19.0 -> 17.5 us). A separate instantiation, since the per-item choice costs the
+// passes without shared prefixes 0.7-1.7 us.
+template <int NT, bool QKV, bool CASC = false>
 __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
     const AttnItem* __restrict__ items, const uint32_t* pos,
     const uint32_t* __restrict__ pages, const _Float16* kc, const _Float16* vc,
@@ -960,6 +967,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
   int pid = 0;  // page id of block wb0 + lane
   if (static_cast<uint32_t>(lane) < nblk) pid = static_cast<int>(pt[(wb0 + lane) >> bpp_shift]);
   const int key_end = static_cast<int>(wb1 * 16);
+  const bool shared_blocks = (it.pref_info & kPrefixItem) != 0;
 
   BlockRegs s0, s1;
   // Loads block b (relative to wb0; wave-uniform) into r; past nblk it reads nothing.
@@ -968,7 +976,14 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
     const uint32_t page = static_cast<uint32_t>(__builtin_amdgcn_readlane(pid, static_cast<int>(valid ? b : 0)));
     const size_t o = (static_cast<size_t>(page) * hkv + kh) * head_stride +
                      static_cast<size_t>((wb0 + b) & bpp_mask) * 16 * kD;
-    load_block_buf(r, kc + o, vc + o, valid, lane);
+    if constexpr (CASC) {
+      if (shared_blocks)  // uniform: a shared prefix, read by the other prefix groups too
+        load_block_buf<0>(r, kc + o, vc + o, valid, lane);
+      else
+        load_block_buf(r, kc + o, vc + o, valid, lane);
+    } else {
+      load_block_buf(r, kc + o, vc + o, valid, lane);
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
 

@@ -687,14 +687,17 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     else YX_LAUNCH_BAL(false, 4, knew, vnew, yx::QkvIn{});
 #undef YX_LAUNCH_BAL
   } else if (plan->wide) {
-#define YX_LAUNCH_WIDE(NT, QKV, KN, VN, IN)                                                         \
-  hipLaunchKernelGGL((yx::paged_attn_decode_wide<NT, QKV>), grid, dim3(64 * yx::kWideWaves), 0,     \
+#define YX_LAUNCH_WIDE(NT, QKV, KN, VN, IN, CASC)                                                   \
+  hipLaunchKernelGGL((yx::paged_attn_decode_wide<NT, QKV, CASC>), grid, dim3(64 * yx::kWideWaves), 0, \
                      c->stream, items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml,     \
                      cnt, KN, VN, static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer],        \
                      kv->v[layer], po_bytes, pml_bytes, H, HK, P, W, scale_log2, IN, mem)
-    if (qkv) YX_LAUNCH_WIDE(1, true, nullptr, nullptr, *qkv);
-    else if (plan->nt <= 2) YX_LAUNCH_WIDE(1, false, knew, vnew, yx::QkvIn{});
-    else YX_LAUNCH_WIDE(2, false, knew, vnew, yx::QkvIn{});
+    const bool casc = plan->cascades > 0;  // shared prefixes only in one-tile passes
+    if (qkv && casc) YX_LAUNCH_WIDE(1, true, nullptr, nullptr, *qkv, true);
+    else if (qkv) YX_LAUNCH_WIDE(1, true, nullptr, nullptr, *qkv, false);
+    else if (plan->nt <= 2 && casc) YX_LAUNCH_WIDE(1, false, knew, vnew, yx::QkvIn{}, true);
+    else if (plan->nt <= 2) YX_LAUNCH_WIDE(1, false, knew, vnew, yx::QkvIn{}, false);
+    else YX_LAUNCH_WIDE(2, false, knew, vnew, yx::QkvIn{}, false);
 #undef YX_LAUNCH_WIDE
   } else switch (plan->nt) {
     case 1: YX_LAUNCH_DECODE(1); break;
