@@ -367,6 +367,7 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
         kv = hip.new_kv(layers, pool, PAGE, HKV, D)
         _fill_arena(hip, kv, layers, SEED + 5)
         us_verify = _time_layers(hip, kv, pr, layers, HQ, [0] * layers, steps) / layers
+        ba_one, ba_two = _time_backend_attention(hip, kv, pr, layers, steps)
         t0 = time.perf_counter()
         copies = []
         forks = [cache.fork(s, cache.seq_len(s) - 3, copies) for s in seqs[:8]]
@@ -379,6 +380,8 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
         copy_us = hip.timer_stop() * 1000.0
         bytes_verify = sum(4096 for _ in seqs) * HKV * D * 2 * 2
         res["cfg5_verify_fork"] = {"us_per_layer_step_verify": round(us_verify, 2),
+                                   "backend_attention_us_one_launch": round(ba_one, 2),
+                                   "backend_attention_us_two_launches": round(ba_two, 2),
                                    "verify_logical_GBs": round(bytes_verify / us_verify / 1e3, 1),
                                    "fork_copies": len(copies), "copy_us_all_layers": round(copy_us, 2),
                                    "host_fork_rollback_us": round(host_us, 1)}

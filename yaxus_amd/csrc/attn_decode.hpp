@@ -916,14 +916,10 @@ struct WideShared {
   float4 o[kWideWaves][NT * 16][kD / 4];
   uint32_t last;
 };
-template <int NT>
-struct WideShared<NT, true> : WideShared<NT, false> {
-  float q[NT * 16][kD];           // the group's queries, normalised and rotated here
-  float qsq[kWideWaves][kD];      // per-wave scratch of that step
-};
-
-// QKV (one tile only): as in the queue kernel, the workgroup runs write_rows for its
-// rows first (queries into LDS, the last chunk's item stores the rows' K/V).
+// QKV: as in the queue kernel, the workgroup runs write_rows for its rows first
+// (queries into LDS, the last chunk's item stores the rows' K/V). The queries and the
+// sum-of-squares scratch borrow the space of the waves' partial results, which is
+// written only after every wave has taken its queries into registers.
 // CASC: the pass has shared-prefix items, whose blocks other prefix items read as well:
 // those load with the default cache policy (kept in L2) instead of nontemporal (cfg2:
 // 19.0 -> 17.5 us). A separate instantiation, since the per-item choice costs the
@@ -939,8 +935,10 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
     uint32_t part_o_bytes, uint32_t part_ml_bytes, uint32_t hq, uint32_t hkv,
     uint32_t bpp_shift, uint32_t window, float scale_log2, QkvIn qi_in,
     const SubRef* __restrict__ members) {
-  static_assert(!QKV || NT == 1, "write_rows is fused for one tile only (LDS)");
-  __shared__ WideShared<NT, QKV> sh;
+  __shared__ WideShared<NT, false> sh;
+  static_assert(sizeof(sh.o) >= (NT * 16 + kWideWaves) * kD * sizeof(float), "q and scratch fit");
+  float (*const q_lds)[kD] = reinterpret_cast<float (*)[kD]>(&sh.o[0][0][0]);
+  float* const qsq_lds = reinterpret_cast<float*>(&sh.o[0][0][0]) + NT * 16 * kD;
   const AttnItem it = items[blockIdx.x];
   const uint32_t kh = blockIdx.y;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -950,8 +948,8 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
   const uint32_t nlog = it.nrows * G;  // logical rows in the group (at most NT * 16)
 
   if constexpr (QKV)
-    fused_write_rows<kWideWaves>(it, kh, G, hq, hkv, nlog, bpp_shift, pos, kv_slot, qi_in, sh.q,
-                                 sh.qsq[wave], wave, lane, kw, vw);
+    fused_write_rows<kWideWaves>(it, kh, G, hq, hkv, nlog, bpp_shift, pos, kv_slot, qi_in, q_lds,
+                                 qsq_lds + wave * kD, wave, lane, kw, vw);
   else if (knew != nullptr && it.chunk == it.nch - 1 && !(it.pref_info & kPrefixItem))
     fused_append<64 * kWideWaves>(it, kh, hkv, bpp_shift, knew, vnew, kv_slot, kw, vw);
 
@@ -1000,7 +998,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
     rpos[t] = lr < nlog ? p : -1;
     rlo[t] = (window > 0 && p + 1 > static_cast<int>(window)) ? p + 1 - static_cast<int>(window) : 0;
     const float* qp;
-    if constexpr (QKV) qp = &sh.q[lrc][g * 8];
+    if constexpr (QKV) qp = &q_lds[lrc][g * 8];
     else qp = q + (static_cast<size_t>(rr) * hq + h) * kD + g * 8;
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
@@ -1029,6 +1027,8 @@ __global__ __launch_bounds__(64 * kWideWaves) void paged_attn_decode_wide(
       }
     }
   }
+  // Every wave holds its queries before any wave writes its partial result over them.
+  if constexpr (QKV) __syncthreads();
 
   float m[NT], l[NT];
   floatx4 acc[NT][8];
