@@ -1,6 +1,6 @@
 """Benchmark of the paged decode path on one MI355X.
 
-Workload (BASELINE headline): B=16 requests, each with ctx 4096 after appending one
+Workload (the headline benchmark): B=16 requests, each with ctx 4096 after appending one
 token (4095 prior + 1), 16 query heads / 4 KV heads, head_dim 128, f16 KV with f32
 accumulation, page size 16, pages scattered over an 8192-page pool by the host
 allocator, 24 layers with distinct arenas (~6.4 GB, far beyond the 256 MB MALL). One
@@ -309,7 +309,7 @@ def cfg5_pass(KvCache):
 
 
 def bench_configs(hip, steps=10, include_long=True, only=None):
-    """BASELINE configurations 2-5 at full size (one JSON object per configuration);
+    """Benchmark configurations 2-5 at full size (one JSON object per configuration);
     `only`: a set of names among cfg2, cfg3, cfg4, cfg5, f32 to run (all when None)."""
     from yaxus_amd import KvCache
     from yaxus_amd.data import uniform_ints
@@ -435,7 +435,7 @@ def main():
     ap.add_argument("--only", default=None,
                     help="with --configs: comma-separated subset of cfg2,cfg3,cfg4,cfg5,f32")
     ap.add_argument("--configs", action="store_true",
-                    help="also measure BASELINE configurations 2-5 at full size (adds ~2 min)")
+                    help="also measure benchmark configurations 2-5 at full size (adds ~2 min)")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the 24 layers one call at a time instead of replaying a HIP graph")
     args = ap.parse_args()

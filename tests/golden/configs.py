@@ -1,4 +1,4 @@
-"""The BASELINE configurations as scenarios, at the sizes the oracle finishes in
+"""The benchmark configurations as scenarios, at the sizes the oracle finishes in
 seconds (configuration 1 at full size; 2-5 shrunk, same shapes of work).
 
 One driver runs each scenario against any (cache, backend) pair: the oracle cache

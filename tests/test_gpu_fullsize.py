@@ -1,4 +1,4 @@
-"""BASELINE configurations at their full sizes, every row against the oracle.
+"""The benchmark configurations at their full sizes, every row against the oracle.
 
 The passes are the benchmark's own (bench.py's builders over the product allocator);
 the arena is filled on the device (yx_fill_normal), the rows' q/k/v are seeded N(0,1)
