@@ -434,12 +434,13 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
     return true;
   };
   // Mid-size passes whose split is not exact anyway: work items of at least
-  // kMinItemBlocks blocks (six per wave) while that still gives work to more than half
+  // kMinItemBlocks blocks (five per wave) while that still gives work to more than half
   // the CUs; shorter items spend more of their time in the start and the split-K
-  // hand-off than they save in parallelism (cfg2, 8.2k blocks: 33-block items 22.0 us,
-  // 52-block items 19.1; B=6 ctx 4096: 20.6 -> 15.5). Exact splits (the headline; B=8,
-  // ctx 4096) and small passes keep one item per CU.
-  constexpr size_t kMinItemBlocks = 48;
+  // hand-off than they save in parallelism (B=12 ctx 2048, 6.1k blocks: 24-block items
+  // 19.9 us, 40-block items 13.8; B=6 ctx 4096 20.5 -> 15.0; cfg2 22.0 -> 17.7; 48- and
+  // 56-block minimums measured slower). Exact splits (the headline; B=8, ctx 4096) and
+  // small passes keep one item per CU.
+  constexpr size_t kMinItemBlocks = 40;
   if (c->target_waves == 0 && nt == 1 && work >= static_cast<size_t>(c->cus) * kMinItemBlocks / 2 &&
       !exact_split(cb))
     cb = std::max<size_t>(cb, kMinItemBlocks);
