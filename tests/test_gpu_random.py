@@ -60,6 +60,7 @@ def test_random_forked_pass_matches_oracle(hip, seed):
     suffix = [[int(x) for x in rng.integers(0, 500, n)] for n in nfork]
     loners = [int(x) for x in rng.integers(0, 900, int(rng.integers(0, 3)))]
     rows = int(rng.choice([1, 1, 2]))
+    mixed = bool(rng.integers(2))  # rows per sequence drawn per sequence (1 or 2)
     window = 0 if rng.integers(3) else int(rng.integers(200, 3000))
     need = sum((p + page - 1) // page for p in prompts) + sum(
         (p + s + rows + page - 1) // page + 1 for p, ss in zip(prompts, suffix) for s in ss) + sum(
@@ -85,7 +86,7 @@ def test_random_forked_pass_matches_oracle(hip, seed):
                 sc.prefill({s: n})
             seqs.append(s)
         order = [seqs[i] for i in rng.permutation(len(seqs))] if rng.integers(2) else seqs
-        pr = sc.run_pass([(s, rows) for s in order])
+        pr = sc.run_pass([(s, int(rng.integers(1, 3)) if mixed else rows) for s in order])
         n = len(pr.meta.pos)
         k = sc.draw(n * hkv * D).reshape(n, hkv, D)
         v = sc.draw(n * hkv * D).reshape(n, hkv, D)
@@ -93,7 +94,7 @@ def test_random_forked_pass_matches_oracle(hip, seed):
         got = sc.hip.attend_append(sc.kv, 0, k, v, q, hq, window=window)
         sc.orc[0].store(pr.meta.kv_slot, k.reshape(n, -1), v.reshape(n, -1))
         want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
-        case = f"heads {hq}/{hkv} page {page} prompts {prompts} suffix {suffix} rows {rows} window {window}"
+        case = f"heads {hq}/{hkv} page {page} prompts {prompts} suffix {suffix} rows {rows} mixed {mixed} window {window}"
         assert close(got, want).all(), f"{case}: max abs err {np.abs(got - want).max()}"
     finally:
         sc.kv.destroy()
