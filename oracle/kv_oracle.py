@@ -7,7 +7,7 @@ never used by it. Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'
 ``cpu_baseline`` leg may import anything under ``oracle/``.
 
 Pinned by: the reference's own unit tests, restated as known-answer tests in
-``tests/test_kv_oracle.py`` (kv.rs:365-403; lib.rs:725-775; the engine admission
+``tests/test_kv_host.py`` (kv.rs:365-403; lib.rs:725-775; the engine admission
 tests engine/mod.rs:969-1030 at the allocator level), and by invariants checked over
 random operation sequences (refcount = number of page-table occurrences, the free
 list is exactly the pages with refcount 0, slots are ``pages[pos // P] * P + pos % P``).

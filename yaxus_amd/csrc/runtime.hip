@@ -34,13 +34,20 @@ int fail(int code, const std::string& m) {
   } while (0)
 
 // A device buffer that only grows. Growing waits for the stream (the old buffer may
-// still be read by queued work) and frees the old allocation.
+// still be read by queued work) and frees the old allocation; it is refused while the
+// stream is being captured into a graph (none of those calls may be captured).
 struct DevBuf {
   void* p = nullptr;
   size_t cap = 0;
   uint64_t gen = 0;  // (re)allocations and releases so far: a captured graph's check
   int ensure(size_t bytes, hipStream_t s, bool zero = false) {
     if (bytes <= cap) return YX_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    YX_HIP(hipStreamIsCapturing(s, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(YX_ERR_INVALID,
+                  "a scratch buffer would have to grow during graph capture: run the call once "
+                  "with these sizes before capturing it");
     ++gen;
     size_t n = std::max(bytes, cap * 2);
     n = (n + 255) & ~static_cast<size_t>(255);
@@ -175,6 +182,26 @@ struct yx_ctx {
   DevBuf d_pos, d_slot, d_pages;
   bool have_pass = false;
   std::map<std::tuple<size_t, size_t, size_t, bool, size_t>, AttnPlan> plans;  // (window, hq, hkv, f32, page)
+  // Work-list buffers of dropped plans, reused by the next pass's plans: a new pass
+  // uploads into them on the stream, after the launches that read them, so it needs
+  // neither a hipFree (which waits for the device) nor a hipMalloc.
+  std::vector<DevBuf> spare;
+  DevBuf take_spare() {
+    if (spare.empty()) return DevBuf{};
+    DevBuf b = spare.back();
+    spare.pop_back();
+    return b;
+  }
+  // Drops the cached plans (a new pass or option), keeping their device buffers.
+  void retire_plans() {
+    for (auto& kv : plans)
+      for (DevBuf* b : {&kv.second.d_items, &kv.second.d_members})
+        if (b->p) {
+          spare.push_back(*b);
+          *b = DevBuf{};
+        }
+    plans.clear();
+  }
   // scratch
   DevBuf part_o, part_ml, counters, io_a, io_b, io_c, io_q;
   // options
@@ -296,6 +323,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
                      });
     auto& p = c->plans[key];
     p = std::move(plan);
+    p.d_items = c->take_spare();
     int rc = p.d_items.ensure(p.pitems.size() * sizeof(yx::PrefillItem), c->stream);
     if (rc) return rc;
     rc = c->staging[c->cur_staging].upload(p.d_items.p, p.pitems.data(),
@@ -562,6 +590,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
   if (plan.items.size() > 0x7fffffff) return fail(YX_ERR_UNSUPPORTED, "too many work items");
   auto& p = c->plans[key];
   p = std::move(plan);
+  p.d_items = c->take_spare();
   int rc = p.d_items.ensure(p.items.size() * sizeof(yx::AttnItem), c->stream);
   if (rc) return rc;
   rc = c->staging[c->cur_staging].upload(p.d_items.p, p.items.data(),
@@ -569,6 +598,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
   if (rc) return rc;
   p.cascades = cascs.size();
   if (!p.members.empty()) {
+    p.d_members = c->take_spare();
     if ((rc = p.d_members.ensure(p.members.size() * sizeof(yx::SubRef), c->stream))) return rc;
     rc = c->staging[c->cur_staging].upload(p.d_members.p, p.members.data(),
                                            p.members.size() * sizeof(yx::SubRef), c->stream);
@@ -827,6 +857,8 @@ int yx_ctx_destroy(yx_ctx* c) {
     kv.second.d_items.release();
     kv.second.d_members.release();
   }
+  for (DevBuf& b : c->spare) b.release();
+  c->spare.clear();
   for (DevBuf* b : {&c->d_pos, &c->d_slot, &c->d_pages, &c->part_o, &c->part_ml, &c->counters,
                     &c->io_a, &c->io_b, &c->io_c, &c->io_q})
     b->release();
@@ -869,11 +901,7 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
   else
     return fail(YX_ERR_INVALID, std::string("unknown option ") + key);
   ++c->epoch;
-  for (auto& kv : c->plans) {
-    kv.second.d_items.release();
-    kv.second.d_members.release();
-  }
-  c->plans.clear();
+  c->retire_plans();
   return YX_OK;
 }
 
@@ -1074,11 +1102,7 @@ int yx_pass_begin(yx_ctx* c, size_t rows, const uint32_t* pos, const uint32_t* k
   if (rc) return rc;
   c->have_pass = false;
   ++c->epoch;
-  for (auto& kv : c->plans) {
-    kv.second.d_items.release();
-    kv.second.d_members.release();
-  }
-  c->plans.clear();
+  c->retire_plans();
   c->rows = rows;
   c->npages = npages;
   c->pos.assign(pos, pos + rows);
