@@ -149,6 +149,19 @@ int yx_attention_append_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k
                             const float* v, const float* q, float* out, size_t hq, size_t hkv,
                             size_t window, float scale);
 
+/* No counterpart in the reference: yx_attention_append_dev for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same kernels, arguments and results; the split-K work list, partials and
+ * arrival counters live in the library's static device scratch (16 MiB per GPU, held
+ * until the process ends) instead of buffers of the context, so the call makes no
+ * device or pinned-host allocation (the pass's pinned staging from yx_pass_begin must
+ * hold the work list). A pass whose work list and partials do not fit the scratch is
+ * refused with YX_ERR_UNSUPPORTED. Every call on a GPU shares that GPU's scratch:
+ * calls that overlap on one GPU (other streams or contexts) race. */
+int yx_attention_append_noalloc(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k,
+                                const float* v, const float* q, float* out, size_t hq,
+                                size_t hkv, size_t window, float scale);
+
 /* Device memory and copies on the context's stream (h2d/d2h are synchronous). */
 int yx_dev_alloc(yx_ctx* ctx, size_t bytes, void** out);
 int yx_dev_free(yx_ctx* ctx, void* p);

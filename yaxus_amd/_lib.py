@@ -88,6 +88,7 @@ HIP_SYMBOLS = {
     "yx_attention_dev": (I, [P, P, S, P, P, S, S, S, F]),
     "yx_attention_append": (I, [P, P, S, P, P, P, P, S, S, S, F]),
     "yx_attention_append_dev": (I, [P, P, S, P, P, P, P, S, S, S, F]),
+    "yx_attention_append_noalloc": (I, [P, P, S, P, P, P, P, S, S, S, F]),
     "yx_dev_alloc": (I, [P, S, P]),
     "yx_dev_free": (I, [P, P]),
     "yx_memcpy_h2d": (I, [P, P, P, S]),

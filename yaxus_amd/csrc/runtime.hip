@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -84,6 +85,8 @@ struct Staging {
     used = 0;
     return YX_OK;
   }
+  // Whether `bytes` more fit without growing the buffer.
+  bool fits(size_t bytes) const { return used + ((bytes + 255) & ~static_cast<size_t>(255)) <= cap; }
   int upload(void* dev, const void* src, size_t bytes, hipStream_t s) {
     if (bytes == 0) return YX_OK;
     size_t need = used + ((bytes + 255) & ~static_cast<size_t>(255));
@@ -133,6 +136,10 @@ struct AttnPlan {
   bool fusable = false;  // the append can run inside the attention kernel
   size_t slots = 0;     // partial slots (per kv head)
   size_t counters = 0;  // arrival counters (per kv head)
+  bool uploaded = false;  // d_items / d_members hold the lists
+  size_t item_bytes() const {
+    return prefill ? pitems.size() * sizeof(yx::PrefillItem) : items.size() * sizeof(yx::AttnItem);
+  }
 };
 
 struct Profile {
@@ -155,6 +162,45 @@ __global__ __launch_bounds__(256) void kv_copy_pages_list(CopyList list,
   uint4* d = base + static_cast<size_t>(list.dst[blockIdx.x]) * page_vec16;
   for (uint32_t i = threadIdx.x; i < page_vec16; i += blockDim.x) d[i] = s[i];
 }
+
+// The scratch of the entry point that allocates nothing (yx_attention_append_noalloc):
+// one file-scope device array per GPU, held from the library's load until the process
+// ends. Its device address is taken once per device (hipGetSymbolAddress, at the first
+// context on the device) and used everywhere host code needs the memory: the array's
+// name is only a host-side stand-in. Layout: arrival counters (zeroed at set-up, left at
+// zero by every completed call), then the work list, the shared-prefix member list, the
+// partial maxima/sums and the partial outputs, each 256-byte aligned.
+constexpr size_t kScratchBytes = size_t{16} << 20;
+constexpr size_t kScratchCounterBytes = size_t{64} << 10;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+__global__ void zero_u32(uint32_t* p, uint32_t n) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+// With `device` current: the scratch's address on it (once per device), counters zeroed.
+int scratch_init(int device, hipStream_t s) {
+  if (device < 0 || device >= kMaxDevices) return fail(YX_ERR_UNSUPPORTED, "device index beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return YX_OK;
+  void* ptr = nullptr;
+  YX_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  if (!ptr) return fail(YX_ERR_HIP, "no device address for the scratch array");
+  hipLaunchKernelGGL(zero_u32, dim3(16), dim3(256), 0, s, static_cast<uint32_t*>(ptr),
+                     static_cast<uint32_t>(kScratchCounterBytes / 4));
+  YX_HIP(hipGetLastError());
+  YX_HIP(hipStreamSynchronize(s));
+  g_scratch_ptr[device] = ptr;
+  return YX_OK;
+}
+
+struct ScratchMap {
+  void *counters, *items, *members, *part_ml, *part_o;
+};
 
 }  // namespace
 
@@ -243,6 +289,31 @@ struct yx_ctx {
 
 namespace {
 
+// Regions of the device's scratch for one no-alloc call; refuses sizes beyond it.
+int scratch_map(yx_ctx* c, size_t items, size_t members, size_t part_ml, size_t part_o,
+                size_t counters, ScratchMap* m) {
+  char* base = static_cast<char*>(g_scratch_ptr[c->device]);
+  if (!base) return fail(YX_ERR_INVALID, "scratch not set up on this device");
+  if (counters > kScratchCounterBytes)
+    return fail(YX_ERR_UNSUPPORTED, "no-alloc call: the pass needs more arrival counters than the scratch holds");
+  auto r256 = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
+  size_t off = kScratchCounterBytes;
+  m->counters = base;
+  m->items = base + off;
+  off += r256(items);
+  m->members = base + off;
+  off += r256(members);
+  m->part_ml = base + off;
+  off += r256(part_ml);
+  m->part_o = base + off;
+  off += r256(part_o);
+  if (off > kScratchBytes)
+    return fail(YX_ERR_UNSUPPORTED, "no-alloc call: the pass's work list and split-K partials need " +
+                                        std::to_string(off) + " bytes, more than the " +
+                                        std::to_string(kScratchBytes) + "-byte scratch");
+  return YX_OK;
+}
+
 int prof_begin(yx_ctx* c, int which, hipEvent_t* e0) {
   *e0 = nullptr;
   if (!c->profiling) return YX_OK;
@@ -323,12 +394,6 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
                      });
     auto& p = c->plans[key];
     p = std::move(plan);
-    p.d_items = c->take_spare();
-    int rc = p.d_items.ensure(p.pitems.size() * sizeof(yx::PrefillItem), c->stream);
-    if (rc) return rc;
-    rc = c->staging[c->cur_staging].upload(p.d_items.p, p.pitems.data(),
-                                           p.pitems.size() * sizeof(yx::PrefillItem), c->stream);
-    if (rc) return rc;
     *out = &p;
     return YX_OK;
   }
@@ -590,21 +655,29 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
   if (plan.items.size() > 0x7fffffff) return fail(YX_ERR_UNSUPPORTED, "too many work items");
   auto& p = c->plans[key];
   p = std::move(plan);
-  p.d_items = c->take_spare();
-  int rc = p.d_items.ensure(p.items.size() * sizeof(yx::AttnItem), c->stream);
-  if (rc) return rc;
-  rc = c->staging[c->cur_staging].upload(p.d_items.p, p.items.data(),
-                                         p.items.size() * sizeof(yx::AttnItem), c->stream);
-  if (rc) return rc;
   p.cascades = cascs.size();
-  if (!p.members.empty()) {
-    p.d_members = c->take_spare();
-    if ((rc = p.d_members.ensure(p.members.size() * sizeof(yx::SubRef), c->stream))) return rc;
-    rc = c->staging[c->cur_staging].upload(p.d_members.p, p.members.data(),
-                                           p.members.size() * sizeof(yx::SubRef), c->stream);
+  *out = &p;
+  return YX_OK;
+}
+
+// The device copy of a plan's work list (and shared-prefix member list), uploaded once
+// per pass into buffers of the context (reused across passes).
+int upload_plan(yx_ctx* c, AttnPlan* p) {
+  if (p->uploaded) return YX_OK;
+  const void* items = p->prefill ? static_cast<const void*>(p->pitems.data()) : p->items.data();
+  const size_t ib = p->item_bytes();
+  p->d_items = c->take_spare();
+  int rc = p->d_items.ensure(std::max<size_t>(ib, 16), c->stream);
+  if (rc) return rc;
+  if ((rc = c->staging[c->cur_staging].upload(p->d_items.p, items, ib, c->stream))) return rc;
+  if (!p->members.empty()) {
+    p->d_members = c->take_spare();
+    if ((rc = p->d_members.ensure(p->members.size() * sizeof(yx::SubRef), c->stream))) return rc;
+    rc = c->staging[c->cur_staging].upload(p->d_members.p, p->members.data(),
+                                           p->members.size() * sizeof(yx::SubRef), c->stream);
     if (rc) return rc;
   }
-  *out = &p;
+  p->uploaded = true;
   return YX_OK;
 }
 
@@ -617,9 +690,13 @@ int qk_rope_impl(yx_ctx* c, yx_kv* kv, size_t layer, const yx::QkvIn& in, size_t
 // the same kernel when the plan allows it, else by the append kernel before it); with
 // qkv, write_rows runs first (in the same kernel when the plan allows it, else as its
 // own launch into a scratch q).
+// noalloc: the work list, partials and counters live in the library's static scratch
+// array instead of buffers of the context, so the call allocates no device or pinned
+// memory (the entry point that allocates nothing).
 int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* out, size_t hq,
                    size_t hkv, size_t window, float scale, const float* knew = nullptr,
-                   const float* vnew = nullptr, const yx::QkvIn* qkv = nullptr) {
+                   const float* vnew = nullptr, const yx::QkvIn* qkv = nullptr,
+                   bool noalloc = false) {
   int rc = check_kv(c, kv, layer);
   if (rc) return rc;
   if (hkv != kv->hkv) return fail(YX_ERR_INVALID, "hkv differs from the arena's");
@@ -632,12 +709,50 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   if ((rc = build_plan(c, window, hq, hkv, kv->f32, kv->page, &plan))) return rc;
   // Logical rows per partial slot: the kernel's tile rows.
   const size_t rps = plan->wide ? static_cast<size_t>((plan->nt + 1) / 2) * 16 : static_cast<size_t>(plan->nt) * 8;
-  if ((rc = c->part_o.ensure(std::max<size_t>(1, plan->slots * hkv * rps * 128 * 4), c->stream)))
-    return rc;
-  if ((rc = c->part_ml.ensure(std::max<size_t>(1, plan->slots * hkv * rps * 8), c->stream)))
-    return rc;
-  if ((rc = c->counters.ensure(std::max<size_t>(1, plan->counters * hkv * 4), c->stream, true)))
-    return rc;
+  const size_t po_need = plan->slots * hkv * rps * 128 * 4, pml_need = plan->slots * hkv * rps * 8;
+  const size_t cnt_need = plan->counters * hkv * 4;
+  const void* d_items;
+  const yx::SubRef* d_members = nullptr;
+  float* po;
+  float2* pml;
+  uint32_t* cnt;
+  size_t po_cap, pml_cap;
+  if (noalloc) {
+    ScratchMap m;
+    if ((rc = scratch_map(c, plan->item_bytes(), plan->members.size() * sizeof(yx::SubRef), pml_need,
+                          po_need, cnt_need, &m)))
+      return rc;
+    // The lists go into the scratch on every call (another call may have used it since),
+    // from the pass's pinned staging, which must have room: it is not grown here.
+    Staging& st = c->staging[c->cur_staging];
+    const void* items = plan->prefill ? static_cast<const void*>(plan->pitems.data()) : plan->items.data();
+    auto r256 = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
+    if (!st.fits(r256(plan->item_bytes()) + r256(plan->members.size() * sizeof(yx::SubRef))))
+      return fail(YX_ERR_UNSUPPORTED, "work list larger than the pass's staging buffer (no-alloc call)");
+    if ((rc = st.upload(m.items, items, plan->item_bytes(), c->stream))) return rc;
+    if (!plan->members.empty() &&
+        (rc = st.upload(m.members, plan->members.data(), plan->members.size() * sizeof(yx::SubRef), c->stream)))
+      return rc;
+    d_items = m.items;
+    d_members = plan->members.empty() ? nullptr : static_cast<const yx::SubRef*>(m.members);
+    po = static_cast<float*>(m.part_o);
+    pml = static_cast<float2*>(m.part_ml);
+    cnt = static_cast<uint32_t*>(m.counters);
+    po_cap = std::max<size_t>(po_need, 16);
+    pml_cap = std::max<size_t>(pml_need, 16);
+  } else {
+    if ((rc = upload_plan(c, plan))) return rc;
+    if ((rc = c->part_o.ensure(std::max<size_t>(1, po_need), c->stream))) return rc;
+    if ((rc = c->part_ml.ensure(std::max<size_t>(1, pml_need), c->stream))) return rc;
+    if ((rc = c->counters.ensure(std::max<size_t>(1, cnt_need), c->stream, true))) return rc;
+    d_items = plan->d_items.p;
+    d_members = plan->members.empty() ? nullptr : static_cast<const yx::SubRef*>(plan->d_members.p);
+    po = static_cast<float*>(c->part_o.p);
+    pml = static_cast<float2*>(c->part_ml.p);
+    cnt = static_cast<uint32_t*>(c->counters.p);
+    po_cap = c->part_o.cap;
+    pml_cap = c->part_ml.cap;
+  }
   if (knew && (plan->prefill || !plan->fusable)) {
     if ((rc = append_impl(c, kv, layer, knew, vnew))) return rc;
     knew = vnew = nullptr;
@@ -662,14 +777,14 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     const dim3 pgrid(static_cast<unsigned>(plan->pitems.size() * hkv));
     if (qkv)
       hipLaunchKernelGGL((yx::paged_attn_prefill<true>), pgrid, dim3(64 * yx::kPrefillWaves), 0, c->stream,
-                       static_cast<const yx::PrefillItem*>(plan->d_items.p),
+                       static_cast<const yx::PrefillItem*>(d_items),
                        static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_pages.p),
                        kv->k[layer], kv->v[layer], q, out, static_cast<uint32_t>(hq),
                        static_cast<uint32_t>(hkv), shift, static_cast<uint32_t>(window),
                        scale * yx::kLog2e, *qkv);
     else
       hipLaunchKernelGGL((yx::paged_attn_prefill<false>), pgrid, dim3(64 * yx::kPrefillWaves), 0, c->stream,
-                       static_cast<const yx::PrefillItem*>(plan->d_items.p),
+                       static_cast<const yx::PrefillItem*>(d_items),
                        static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_pages.p),
                        kv->k[layer], kv->v[layer], q, out, static_cast<uint32_t>(hq),
                        static_cast<uint32_t>(hkv), shift, static_cast<uint32_t>(window),
@@ -685,19 +800,16 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   dim3 grid(static_cast<unsigned>(plan->items.size()), static_cast<unsigned>(hkv));
   hipEvent_t e0;
   if ((rc = prof_begin(c, YX_KERNEL_ATTENTION, &e0))) return rc;
-  const auto* items = static_cast<const yx::AttnItem*>(plan->d_items.p);
+  const auto* items = static_cast<const yx::AttnItem*>(d_items);
   const auto* pos = static_cast<const uint32_t*>(c->d_pos.p);
   const auto* pages = static_cast<const uint32_t*>(c->d_pages.p);
-  auto* po = static_cast<float*>(c->part_o.p);
-  auto* pml = static_cast<float2*>(c->part_ml.p);
-  auto* cnt = static_cast<uint32_t*>(c->counters.p);
   const uint32_t H = static_cast<uint32_t>(hq), HK = static_cast<uint32_t>(hkv);
   uint32_t P = 0;
   while ((16u << P) < kv->page) ++P;  // log2(blocks of 16 keys per page)
   const uint32_t W = static_cast<uint32_t>(window);
-  const uint32_t po_bytes = static_cast<uint32_t>(std::min<size_t>(c->part_o.cap, 0xffffffffu));
-  const uint32_t pml_bytes = static_cast<uint32_t>(std::min<size_t>(c->part_ml.cap, 0xffffffffu));
-  const auto* mem = plan->members.empty() ? nullptr : static_cast<const yx::SubRef*>(plan->d_members.p);
+  const uint32_t po_bytes = static_cast<uint32_t>(std::min<size_t>(po_cap, 0xffffffffu));
+  const uint32_t pml_bytes = static_cast<uint32_t>(std::min<size_t>(pml_cap, 0xffffffffu));
+  const auto* mem = d_members;
 #define YX_LAUNCH_DECODE(NT)                                                                        \
   hipLaunchKernelGGL(yx::paged_attn_decode<NT>, grid, dim3(64 * yx::DecodeWaves<NT>::value), 0,      \
                      c->stream, items, pos, pages,                                                  \
@@ -839,6 +951,10 @@ int yx_ctx_create(int device, yx_ctx** out) {
   if (e != hipSuccess) {
     delete c;
     return fail(YX_ERR_HIP, std::string("context set-up: ") + hipGetErrorString(e));
+  }
+  if (int rc = scratch_init(device, c->stream)) {
+    yx_ctx_destroy(c);
+    return rc;
   }
   *out = c;
   return YX_OK;
@@ -1217,6 +1333,16 @@ int yx_attention_append_dev(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, 
   int rc = c->set_device();
   if (rc) return rc;
   return attention_impl(c, kv, layer, q, out, hq, hkv, window, scale, k, v);
+}
+
+int yx_attention_append_noalloc(yx_ctx* c, yx_kv* kv, size_t layer, const float* k,
+                                const float* v, const float* q, float* out, size_t hq,
+                                size_t hkv, size_t window, float scale) {
+  if (!c || !kv) return fail(YX_ERR_INVALID, "null argument");
+  if (!k || !v) return fail(YX_ERR_INVALID, "null k or v");
+  int rc = c->set_device();
+  if (rc) return rc;
+  return attention_impl(c, kv, layer, q, out, hq, hkv, window, scale, k, v, nullptr, true);
 }
 
 int yx_attention_append(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float* v,
