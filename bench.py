@@ -513,11 +513,14 @@ def main():
         step()
     hip.profile(False)
     if args.profile_run:
-        # Calibration for FETCH_SIZE / WRITE_SIZE: a plain copy of exactly 1 GiB.
+        # Calibration for FETCH_SIZE / WRITE_SIZE: a plain copy of exactly 1 GiB (1 GiB
+        # read, 1 GiB written), then a read-only pass over 1 GiB (yx_dev_checksum).
         src, dst = hip.tensor((1 << 30,), np.uint8), hip.tensor((1 << 30,), np.uint8)
         for _ in range(3):
             hip.L.yx_dev_copy(hip.ctx, dst.ptr, src.ptr, 1 << 30)
         hip.sync()
+        for _ in range(3):
+            hip.checksum(src.ptr, 1 << 30)
         src.free()
         dst.free()
     attn_ms, attn_n = hip.profile_read(YX_KERNEL_ATTENTION)

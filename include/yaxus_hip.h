@@ -169,6 +169,10 @@ int yx_memcpy_h2d(yx_ctx* ctx, void* dst, const void* src, size_t bytes);
 int yx_memcpy_d2h(yx_ctx* ctx, void* dst, const void* src, size_t bytes);
 /* Plain device copy kernel (also the reference point for HBM byte counters). */
 int yx_dev_copy(yx_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* XOR of every 8-byte word of a device buffer (size and pointer 16-byte aligned),
+ * synchronous: an order-independent checksum of device data, and a read-only pass over
+ * the buffer (the read-side reference point for the HBM byte counters). */
+int yx_dev_checksum(yx_ctx* ctx, const void* src, size_t bytes, uint64_t* out);
 /* Synthetic N(0,1) values: splitmix64 -> Box-Muller, element i of stream `seed` at
  * index offset + i (see yaxus_amd/data.py for the definition); dtype f32 or f16. */
 int yx_fill_normal(yx_ctx* ctx, void* dst, size_t n, int dtype, uint64_t seed, uint64_t offset);

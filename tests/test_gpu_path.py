@@ -399,3 +399,17 @@ def test_attention_in_one_launch_equals_two(hip, hq, hkv, lens, k):
     qo = sc.orc[0].write_rows(qkv, hq, qn, kn, 1e-6, f, 1.0, pr.meta.pos, pr.meta.kv_slot)
     want = sc.orc[0].attend(qo, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
     assert close(outs[0], want).all(), f"max abs err {np.abs(outs[0] - want).max()}"
+
+
+def test_dev_checksum_is_the_xor_of_the_words(hip):
+    """yx_dev_checksum = XOR of every 8-byte word (numpy), including a size that leaves
+    threads without work and the empty buffer."""
+    rng = np.random.default_rng(11)
+    for n in (16, 4096 + 48, 1 << 22):
+        a = rng.integers(0, 2**63, size=n // 8, dtype=np.uint64)
+        t = hip.tensor((n,), np.uint8).upload(a.view(np.uint8))
+        try:
+            assert hip.checksum(t.ptr, n) == int(np.bitwise_xor.reduce(a))
+        finally:
+            t.free()
+    assert hip.checksum(None, 0) == 0

@@ -94,6 +94,7 @@ HIP_SYMBOLS = {
     "yx_memcpy_h2d": (I, [P, P, P, S]),
     "yx_memcpy_d2h": (I, [P, P, P, S]),
     "yx_dev_copy": (I, [P, P, P, S]),
+    "yx_dev_checksum": (I, [P, P, S, P]),
     "yx_fill_normal": (I, [P, P, S, I, U64, U64]),
     "yx_graph_begin": (I, [P]),
     "yx_graph_end": (I, [P]),

@@ -289,6 +289,12 @@ class HipBackend:
                                              hq, kv.hkv, w, scale))
         return o
 
+    def checksum(self, dev_ptr, nbytes):
+        """XOR of every 8-byte word of a device buffer (yx_dev_checksum)."""
+        out = ctypes.c_uint64()
+        check_hip(self.L.yx_dev_checksum(self.ctx, dev_ptr, nbytes, ctypes.byref(out)))
+        return out.value
+
     def fill_normal(self, dev_ptr, n, f16, seed, offset=0):
         check_hip(self.L.yx_fill_normal(self.ctx, dev_ptr, n,
                                         _lib.YX_DTYPE_F16 if f16 else _lib.YX_DTYPE_F32,

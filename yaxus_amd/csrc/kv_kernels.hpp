@@ -75,6 +75,26 @@ __global__ __launch_bounds__(256) void dev_copy16(uint4* __restrict__ d,
     d[i] = s[i];
 }
 
+// XOR of every 8-byte word of a buffer (n 16-byte pieces): a read-only pass over the
+// buffer (the read-side reference point for the HBM byte counters) and an
+// order-independent checksum of device data.
+__global__ __launch_bounds__(256) void dev_checksum16(const uint4* __restrict__ s, size_t n,
+                                                      unsigned long long* out) {
+  unsigned long long x = 0;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    typedef uint32_t w4 __attribute__((ext_vector_type(4)));
+    const w4 v = __builtin_nontemporal_load(reinterpret_cast<const w4*>(s) + i);
+    x ^= (static_cast<unsigned long long>(v.y) << 32 | v.x) ^ (static_cast<unsigned long long>(v.w) << 32 | v.z);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x ^= __shfl_xor(x, off);
+  __shared__ unsigned long long part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) atomicXor(out, part[0] ^ part[1] ^ part[2] ^ part[3]);
+}
+
 __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
   x += 0x9e3779b97f4a7c15ull;
   x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;

@@ -1419,6 +1419,27 @@ int yx_dev_copy(yx_ctx* c, void* dst, const void* src, size_t bytes) {
   return YX_OK;
 }
 
+int yx_dev_checksum(yx_ctx* c, const void* src, size_t bytes, uint64_t* out) {
+  if (!c || !out) return fail(YX_ERR_INVALID, "null argument");
+  if (bytes && !src) return fail(YX_ERR_INVALID, "null buffer");
+  if (bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16)
+    return fail(YX_ERR_INVALID, "dev_checksum needs a 16-byte aligned size and pointer");
+  int rc = c->set_device();
+  if (rc) return rc;
+  *out = 0;
+  if (bytes == 0) return YX_OK;
+  if ((rc = c->io_c.ensure(16, c->stream))) return rc;
+  YX_HIP(hipMemsetAsync(c->io_c.p, 0, 8, c->stream));
+  const size_t n = bytes / 16;
+  const unsigned blocks = static_cast<unsigned>(std::min<size_t>((n + 255) / 256, 8192));
+  hipLaunchKernelGGL(yx::dev_checksum16, dim3(blocks), dim3(256), 0, c->stream,
+                     static_cast<const uint4*>(src), n, static_cast<unsigned long long*>(c->io_c.p));
+  YX_HIP(hipGetLastError());
+  YX_HIP(hipMemcpyAsync(out, c->io_c.p, 8, hipMemcpyDeviceToHost, c->stream));
+  YX_HIP(hipStreamSynchronize(c->stream));
+  return YX_OK;
+}
+
 int yx_fill_normal(yx_ctx* c, void* dst, size_t n, int dtype, uint64_t seed, uint64_t offset) {
   if (!c || !dst) return fail(YX_ERR_INVALID, "null argument");
   if (dtype != YX_DTYPE_F16 && dtype != YX_DTYPE_F32) return fail(YX_ERR_INVALID, "bad dtype");
