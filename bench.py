@@ -401,6 +401,40 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
                                         "GBs": round(nbytes / us / 1e3, 1),
                                         "kv_bytes_per_layer": nbytes}
         kv.destroy()
+    if want('step'):
+        # The step after attention at the headline's decode shape: o_proj (16 rows of
+        # hq * 128 = 2048 against a bf16 [2048][2048] weight) and the greedy pick over a
+        # 151936-token vocabulary.
+        t, k, n, vocab = B, HQ * D, 2048, 151936
+        x, w, o = hip.tensor((t, k)), hip.tensor((n, k), np.uint16), hip.tensor((t, n))
+        hip.fill_normal(x.ptr, t * k, False, SEED + 61, 0)
+        hip.fill_normal(w.ptr, n * k, True, SEED + 62, 0)  # N(0,1) binary16 bits, read as bf16
+        logits, ids = hip.tensor((t, vocab)), hip.tensor((t,), np.uint32)
+        hip.fill_normal(logits.ptr, t * vocab, False, SEED + 63, 0)
+        def graph_us(fn, per_graph=24, reps=20):
+            # A HIP graph of `per_graph` launches (as a decode step would hold them),
+            # replayed: µs per launch, launch gaps inside the graph included.
+            fn()
+            hip.sync()
+            hip.graph_begin()
+            for _ in range(per_graph):
+                fn()
+            hip.graph_end()
+            hip.graph_launch()
+            hip.sync()
+            hip.timer_start()
+            for _ in range(reps):
+                hip.graph_launch()
+            return hip.timer_stop() * 1000.0 / (reps * per_graph)
+
+        mm_us = graph_us(lambda: hip.matmul_bf16(x, w, out=o))
+        am_us = graph_us(lambda: hip.argmax_rows(logits, out=ids))
+        res["step_after_oproj_argmax"] = {
+            "oproj_us": round(mm_us, 2), "oproj_weight_GBs": round(n * k * 2 / mm_us / 1e3, 1),
+            "oproj_shape": [t, k, n], "argmax_us": round(am_us, 2),
+            "argmax_GBs": round(t * vocab * 4 / am_us / 1e3, 1), "argmax_shape": [t, vocab]}
+        for z in (x, w, o, logits, ids):
+            z.free()
     if include_long and want('cfg4'):
         # cfg4: 32 layers, 1 full then 3 sliding (window 2048), repeated.
         cache, pr, pool = cfg4_pass(KvCache)
@@ -436,7 +470,7 @@ def main():
                     help="for rocprofv3: also run a 1 GiB device copy (the byte-counter "
                          "calibration point) and skip the CPU baseline")
     ap.add_argument("--only", default=None,
-                    help="with --configs: comma-separated subset of cfg2,cfg3,cfg4,cfg5,f32")
+                    help="with --configs: comma-separated subset of cfg2,cfg3,cfg4,cfg5,f32,step")
     ap.add_argument("--configs", action="store_true",
                     help="also measure benchmark configurations 2-5 at full size (adds ~2 min)")
     ap.add_argument("--no-graph", action="store_true",

@@ -46,6 +46,7 @@ unsafe extern "C" {
     pub fn yx_ctx_destroy(ctx: *mut yx_ctx) -> c_int;
     pub fn yx_sync(ctx: *mut yx_ctx) -> c_int;
     pub fn yx_ctx_set_option(ctx: *mut yx_ctx, key: *const c_char, value: c_long) -> c_int;
+    pub fn yx_ctx_get_stat(ctx: *mut yx_ctx, key: *const c_char, out: *mut u64) -> c_int;
 
     pub fn yx_kv_create(ctx: *mut yx_ctx, layers: usize, pages: usize, page_size: usize, hkv: usize,
                         head_dim: usize, dtype: c_int, out: *mut *mut yx_kv) -> c_int;
@@ -90,6 +91,11 @@ unsafe extern "C" {
     pub fn yx_attention_append_noalloc(ctx: *mut yx_ctx, kv: *mut yx_kv, layer: usize,
                                        k: *const f32, v: *const f32, q: *const f32, out: *mut f32,
                                        hq: usize, hkv: usize, window: usize, scale: f32) -> c_int;
+
+    pub fn yx_matmul_bf16_dev(ctx: *mut yx_ctx, x: *const f32, w: *const u16, out: *mut f32, t: usize,
+                              k: usize, n: usize) -> c_int;
+    pub fn yx_argmax_rows_dev(ctx: *mut yx_ctx, logits: *const f32, rows: usize, cols: usize,
+                              out: *mut u32) -> c_int;
 
     pub fn yx_dev_alloc(ctx: *mut yx_ctx, bytes: usize, out: *mut *mut c_void) -> c_int;
     pub fn yx_dev_free(ctx: *mut yx_ctx, p: *mut c_void) -> c_int;

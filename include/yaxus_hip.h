@@ -68,6 +68,11 @@ int yx_sync(yx_ctx* ctx);
  * cached work lists. Values are positive; 0 is accepted for attn_target_waves,
  * attn_decode_shape and attn_cascade. */
 int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
+/* Counters of the context since its creation: "page_entries_sent" (page-table entries
+ * yx_pass_begin uploaded) and "page_runs_sent" (runs of consecutive entries they formed).
+ * A pass whose groups keep their order and fit the device regions of the previous pass
+ * sends only the entries that changed. */
+int yx_ctx_get_stat(yx_ctx* ctx, const char* key, uint64_t* out);
 
 /* Backend::new_kv (lib.rs:118; GPU ops/mod.rs:42-66): `layers` layers of `pages`
  * pages of `page_size` tokens (a multiple of 16), zeroed. dtype YX_DTYPE_F16 (binary16,
@@ -94,7 +99,11 @@ int yx_kv_write_pages(yx_ctx* ctx, yx_kv* kv, size_t layer, const uint32_t* page
                       const void* k_in, const void* v_in);
 
 /* Backend::begin_pass (lib.rs:123; GPU ops/mod.rs:76-99): the rows of the next pass.
- * Rows of one sequence are consecutive, share pt_off and have consecutive positions. */
+ * Rows of one sequence are consecutive, share pt_off and have consecutive positions.
+ * The positions, slots and the page-table entries that differ from what the device
+ * holds (the device keeps each sequence's table in a region of its own from pass to
+ * pass), together with the work lists of the attention calls the previous pass made,
+ * go to the device as one copy on the context's stream. */
 int yx_pass_begin(yx_ctx* ctx, size_t rows, const uint32_t* pos, const uint32_t* kv_slot,
                   const uint32_t* pt_off, const uint32_t* pages, size_t npages);
 
@@ -161,6 +170,19 @@ int yx_attention_append_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k
 int yx_attention_append_noalloc(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k,
                                 const float* v, const float* q, float* out, size_t hq,
                                 size_t hkv, size_t window, float scale);
+
+/* The step after the attention (device pointers, asynchronous). Backend::matmul with a
+ * bf16 weight (lib.rs:133; backend-cpu lib.rs:234-248, 314-345), e.g. the output
+ * projection o_proj: out `[t][n]` f32 = x `[t][k]` f32 times w `[n][k]` (bf16 bits)
+ * transposed; k a multiple of 8, x and w 16-byte aligned. Every product is exact (x in
+ * three bf16 parts), the sums are f32. */
+int yx_matmul_bf16_dev(yx_ctx* ctx, const float* x, const uint16_t* w, float* out, size_t t,
+                       size_t k, size_t n);
+/* SyncReadback::argmax_rows (lib.rs:182; backend-cpu lib.rs:432-440, 556-558): out[r] =
+ * the first index of the largest value of row r of logits `[rows][cols]` f32; NaN is
+ * never chosen, and a row with nothing above -inf gives 0. out is a device array of
+ * `rows` u32. */
+int yx_argmax_rows_dev(yx_ctx* ctx, const float* logits, size_t rows, size_t cols, uint32_t* out);
 
 /* Device memory and copies on the context's stream (h2d/d2h are synchronous). */
 int yx_dev_alloc(yx_ctx* ctx, size_t bytes, void** out);

@@ -37,6 +37,9 @@ def lib():
         L.orc_cos_sin.argtypes = [P, S, ctypes.c_float, S, P, P]
         L.orc_dot.argtypes = [P, P, S]
         L.orc_dot.restype = ctypes.c_float
+        L.orc_matmul_bf16.argtypes = [P, S, S, P, S, P]
+        L.orc_argmax.argtypes = [P, S]
+        L.orc_argmax.restype = ctypes.c_uint32
         _LIB = L
     return _LIB
 
@@ -135,3 +138,21 @@ class OracleArena:
         k = self.k[s].reshape(self.page, self.hkv, self.d).transpose(1, 0, 2)
         v = self.v[s].reshape(self.page, self.hkv, self.d).transpose(1, 0, 2)
         return np.ascontiguousarray(k), np.ascontiguousarray(v)
+
+
+def matmul_bf16(x, w_bits):
+    """The CPU backend's matmul with a bf16 weight: x `[t][k]` f32, w `[n][k]` bf16 bits
+    (uint16) -> `[t][n]` f32 (lib.rs:234-248, 314-345)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    t, k = x.shape
+    n = w.shape[0]
+    out = np.empty((t, n), dtype=np.float32)
+    lib().orc_matmul_bf16(_p(x), t, k, _p(w), n, _p(out))
+    return out
+
+
+def argmax_rows(logits):
+    """The CPU backend's argmax of every row (lib.rs:432-440, 556-558)."""
+    a = np.ascontiguousarray(logits, dtype=np.float32)
+    return np.array([lib().orc_argmax(_p(a[r]), a.shape[1]) for r in range(a.shape[0])], np.uint32)

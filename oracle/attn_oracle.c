@@ -9,6 +9,8 @@
  *   - write_rows     crates/yaxus-backend-cpu/src/lib.rs:359-385
  *   - attend         crates/yaxus-backend-cpu/src/lib.rs:389-427 (two-pass softmax)
  *   - copy_page      crates/yaxus-backend-cpu/src/lib.rs:472-479
+ *   - matmul (bf16)  crates/yaxus-backend-cpu/src/lib.rs:234-248, 314-345 (dot_bf16)
+ *   - argmax         crates/yaxus-backend-cpu/src/lib.rs:432-440
  * The KV arena has the reference's layout, slot-major `[slot][hkv * d]` per layer
  * (lib.rs:205-214), stored as f32 or, in f16 mode, as IEEE binary16 bits rounded to
  * nearest-even from f32 (the `half` 2.7.1 crate's rounding). Arithmetic is f32
@@ -110,6 +112,47 @@ float orc_dot(const float* a, const float* b, size_t n) {
   for (int i = 0; i < 16; ++i) s += acc[i];
   for (size_t i = chunks * 16; i < n; ++i) s += a[i] * b[i];
   return s;
+}
+
+/* lib.rs:109-111 (yaxus-model weights.rs): bf16 is the upper half of an f32. */
+static inline float bf16_to_f32(uint16_t b) {
+  union { uint32_t u; float f; } v;
+  v.u = (uint32_t)b << 16;
+  return v.f;
+}
+
+/* lib.rs:234-248 (dot_bf16) inside lib.rs:314-345 (matmul): out[i][j] = w[j] . x[i] with
+ * 16 accumulators over whole chunks of 16, summed in order, then the rest. (For four or
+ * more rows the CPU decodes the row to f32 first and calls dot (lib.rs:280-294): the same
+ * products in the same order, so the same bits.) */
+void orc_matmul_bf16(const float* x, size_t t, size_t k, const uint16_t* w, size_t n, float* out) {
+  for (size_t j = 0; j < n; ++j) {
+    const uint16_t* wr = w + j * k;
+    for (size_t i = 0; i < t; ++i) {
+      const float* xr = x + i * k;
+      float acc[16] = {0};
+      const size_t chunks = k / 16;
+      for (size_t c = 0; c < chunks; ++c)
+        for (int l = 0; l < 16; ++l) acc[l] += bf16_to_f32(wr[c * 16 + l]) * xr[c * 16 + l];
+      float s = 0.0f;
+      for (int l = 0; l < 16; ++l) s += acc[l];
+      for (size_t e = chunks * 16; e < k; ++e) s += bf16_to_f32(wr[e]) * xr[e];
+      out[i * n + j] = s;
+    }
+  }
+}
+
+/* lib.rs:432-440: the first index whose value is strictly larger than every earlier one,
+ * starting from (0, -inf): NaN never wins, a row of -inf / NaN gives 0. */
+uint32_t orc_argmax(const float* row, size_t n) {
+  size_t best = 0;
+  float best_v = -INFINITY;
+  for (size_t i = 0; i < n; ++i)
+    if (row[i] > best_v) {
+      best = i;
+      best_v = row[i];
+    }
+  return (uint32_t)best;
 }
 
 /* lib.rs:296-302 */

@@ -1,0 +1,66 @@
+"""The step after attention on the GPU against the CPU backend's restatement
+(oracle/attn_oracle.c): Backend::matmul with a bf16 weight (the output projection;
+crates/yaxus-backend-cpu/src/lib.rs:234-248, 314-345) within f32 accumulation error of
+the oracle, and argmax_rows (lib.rs:432-440) bit for bit, over the decode shapes and
+edge cases (partial tiles, ties, NaN, infinities, signed zeros, one column)."""
+
+import numpy as np
+import pytest
+
+from oracle.attn import argmax_rows, matmul_bf16, normal
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_bits(a):
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("t,k,n", [(1, 2048, 2048), (16, 2048, 2048), (5, 72, 40), (17, 256, 33),
+                                   (40, 2048, 256), (16, 8, 16), (3, 4096, 1000)])
+def test_matmul_bf16_matches_the_cpu_backend(hip, t, k, n):
+    x = normal(t * k, 31, t * 7 + n).reshape(t, k)
+    w = _bf16_bits(normal(n * k, 32, k + n).reshape(n, k))
+    dx = hip.tensor(x.shape).upload(x)
+    dw = hip.tensor(w.shape, np.uint16).upload(w)
+    try:
+        got = hip.matmul_bf16(dx, dw).numpy()
+    finally:
+        dx.free()
+        dw.free()
+    want = matmul_bf16(x, w)
+    wf = (w.astype(np.uint32) << 16).view(np.float32)
+    # Exact products, f32 sums in another order: within 2 k ulp-weighted magnitudes.
+    bound = 2 * k * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(wf).astype(np.float64).T)
+    assert np.all(np.abs(got.astype(np.float64) - want) <= bound), np.abs(got - want).max()
+
+
+def test_argmax_rows_matches_the_cpu_backend(hip):
+    rng = np.random.default_rng(9)
+    cases = [rng.standard_normal((16, 151936), dtype=np.float32),
+             rng.standard_normal((1, 151936), dtype=np.float32),
+             rng.standard_normal((3, 1), dtype=np.float32),
+             rng.standard_normal((20, 4097), dtype=np.float32)]
+    a = cases[0]
+    a[0, [5, 150000]] = 99.0                # a tie across slices: the first
+    a[1, :] = np.nan                        # all NaN: 0
+    a[2, :] = -np.inf                       # all -inf: 0
+    a[3, 1000] = np.inf
+    a[4, :] = np.nan
+    a[4, 77777] = -3.0                      # one number among NaN
+    a[5, :] = -0.0
+    a[5, 100000] = 0.0                      # equal zeros: the first
+    a[6, ::2] = np.nan                      # NaN interleaved
+    for logits in cases:
+        d = hip.tensor(logits.shape).upload(logits)
+        try:
+            got = hip.argmax_rows(d)
+            np.testing.assert_array_equal(got.numpy(), argmax_rows(logits))
+            got.free()
+            # Again (the arrival counters are back at zero).
+            got = hip.argmax_rows(d)
+            np.testing.assert_array_equal(got.numpy(), argmax_rows(logits))
+            got.free()
+        finally:
+            d.free()

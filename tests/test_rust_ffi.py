@@ -28,6 +28,8 @@ C_TO_RUST = {
     "double*": "*mut f64",
     "const float*": "*const f32",
     "const uint32_t*": "*const u32",
+    "uint32_t*": "*mut u32",
+    "const uint16_t*": "*const u16",
     "uint64_t*": "*mut u64",
     "void*": "*mut c_void",
     "const void*": "*const c_void",

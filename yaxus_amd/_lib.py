@@ -95,6 +95,9 @@ HIP_SYMBOLS = {
     "yx_memcpy_d2h": (I, [P, P, P, S]),
     "yx_dev_copy": (I, [P, P, P, S]),
     "yx_dev_checksum": (I, [P, P, S, P]),
+    "yx_ctx_get_stat": (I, [P, ctypes.c_char_p, P]),
+    "yx_matmul_bf16_dev": (I, [P, P, P, P, S, S, S]),
+    "yx_argmax_rows_dev": (I, [P, P, S, S, P]),
     "yx_fill_normal": (I, [P, P, S, I, U64, U64]),
     "yx_graph_begin": (I, [P]),
     "yx_graph_end": (I, [P]),

@@ -289,6 +289,33 @@ class HipBackend:
                                              hq, kv.hkv, w, scale))
         return o
 
+    def matmul_bf16(self, x, w, out=None):
+        """x `[t][k]` f32 device tensor times w `[n][k]` (bf16 bits, uint16 device tensor)
+        transposed: `[t][n]` f32 (yx_matmul_bf16_dev)."""
+        t, k = x.shape
+        n = w.shape[0]
+        if w.shape[1] != k:
+            raise ValueError("x and w disagree on k")
+        out = out if out is not None else self.tensor((t, n))
+        _need(out, t * n * 4, "out")
+        check_hip(self.L.yx_matmul_bf16_dev(self.ctx, x.ptr, w.ptr, out.ptr, t, k, n))
+        return out
+
+    def argmax_rows(self, logits, out=None):
+        """The first index of each row's largest value (yx_argmax_rows_dev): a uint32
+        device tensor of `rows`."""
+        rows, cols = logits.shape
+        out = out if out is not None else self.tensor((rows,), np.uint32)
+        _need(out, rows * 4, "out")
+        check_hip(self.L.yx_argmax_rows_dev(self.ctx, logits.ptr, rows, cols, out.ptr))
+        return out
+
+    def stat(self, key):
+        """A counter of the context (yx_ctx_get_stat), e.g. "page_entries_sent"."""
+        out = ctypes.c_uint64()
+        check_hip(self.L.yx_ctx_get_stat(self.ctx, key.encode(), ctypes.byref(out)))
+        return out.value
+
     def checksum(self, dev_ptr, nbytes):
         """XOR of every 8-byte word of a device buffer (yx_dev_checksum)."""
         out = ctypes.c_uint64()

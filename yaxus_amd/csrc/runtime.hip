@@ -17,6 +17,7 @@
 #include "attn_prefill.hpp"
 #include "kv_kernels.hpp"
 #include "qk_rope.hpp"
+#include "step_after.hpp"
 
 namespace {
 
@@ -107,6 +108,29 @@ struct Staging {
     used = need;
     return YX_OK;
   }
+  // Room for `bytes` at the start of an empty staging buffer (grown when needed), to be
+  // filled by the caller and sent with send(): one copy for many pieces.
+  int reserve(size_t bytes, char** out) {
+    if (used != 0) return fail(YX_ERR_INVALID, "internal: reserve on a staging buffer in use");
+    if (bytes > cap) {
+      if (done) YX_HIP(hipEventSynchronize(done));
+      if (host) YX_HIP(hipHostFree(host));
+      host = nullptr;
+      cap = 0;
+      const size_t n = std::max(bytes, static_cast<size_t>(1) << 16);
+      YX_HIP(hipHostMalloc(reinterpret_cast<void**>(&host), n, hipHostMallocDefault));
+      cap = n;
+    }
+    *out = host;
+    return YX_OK;
+  }
+  int send(void* dev, size_t bytes, hipStream_t s) {
+    if (bytes) YX_HIP(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, s));
+    if (!done) YX_HIP(hipEventCreateWithFlags(&done, hipEventDisableTiming));
+    YX_HIP(hipEventRecord(done, s));
+    used = (bytes + 255) & ~static_cast<size_t>(255);
+    return YX_OK;
+  }
   void release() {
     if (done) (void)hipEventDestroy(done);
     if (host) (void)hipHostFree(host);
@@ -115,9 +139,22 @@ struct Staging {
   }
 };
 
+// The rows of one sequence in a pass. pt_off: its page table in the pass's host page
+// tables; dev_off: in the device's page tables (a region that stays put across passes).
 struct Group {
-  uint32_t r0, n, pt_off;
+  uint32_t r0, n, pt_off, dev_off;
 };
+
+// Copies page-table runs into the device's page tables: run r writes runs[3r + 1]
+// entries from data[runs[3r + 2]...] to pages[runs[3r]...].
+__global__ __launch_bounds__(256) void page_runs_apply(const uint32_t* __restrict__ runs, uint32_t nruns,
+                                                       const uint32_t* __restrict__ data,
+                                                       uint32_t* __restrict__ pages) {
+  for (uint32_t r = blockIdx.x; r < nruns; r += gridDim.x) {
+    const uint32_t dst = runs[3 * r], n = runs[3 * r + 1], src = runs[3 * r + 2];
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) pages[dst + i] = data[src + i];
+  }
+}
 
 // A split-K work list for one (window, hq, hkv) over the current pass.
 struct AttnPlan {
@@ -136,7 +173,11 @@ struct AttnPlan {
   bool fusable = false;  // the append can run inside the attention kernel
   size_t slots = 0;     // partial slots (per kv head)
   size_t counters = 0;  // arrival counters (per kv head)
-  bool uploaded = false;  // d_items / d_members hold the lists
+  bool uploaded = false;  // dev_items / dev_members hold the lists
+  // Where the kernels read the lists: d_items / d_members, or the pass's metadata buffer
+  // when the plan was built with the pass (yx_pass_begin).
+  const void* dev_items = nullptr;
+  const void* dev_members = nullptr;
   size_t item_bytes() const {
     return prefill ? pitems.size() * sizeof(yx::PrefillItem) : items.size() * sizeof(yx::AttnItem);
   }
@@ -225,7 +266,18 @@ struct yx_ctx {
   std::vector<uint32_t> pos, slot, pt_off, pages;
   std::vector<Group> groups;
   uint32_t max_page = 0, max_slot = 0;
-  DevBuf d_pos, d_slot, d_pages;
+  // Device pass metadata. d_meta: this pass's positions and slots, the page-table runs
+  // that changed since the previous pass, and the work lists built with the pass, sent
+  // as one copy. d_pages: the page tables, one region per group that stays put from pass
+  // to pass while the groups keep their order and fit (a decode step then sends only the
+  // entries that changed: a new page, a copied one).
+  DevBuf d_meta, d_pages;
+  const uint32_t* dev_pos = nullptr;
+  const uint32_t* dev_slot = nullptr;
+  std::vector<uint32_t> region_off, region_cap;  // per group of the previous pass
+  std::vector<uint32_t> dev_mirror;              // what d_pages holds, entry by entry
+  std::vector<std::tuple<size_t, size_t, size_t, bool, size_t>> used_keys;  // plans used this pass
+  uint64_t pages_sent = 0, runs_sent = 0;        // page-table entries and runs uploaded (tests)
   bool have_pass = false;
   std::map<std::tuple<size_t, size_t, size_t, bool, size_t>, AttnPlan> plans;  // (window, hq, hkv, f32, page)
   // Work-list buffers of dropped plans, reused by the next pass's plans: a new pass
@@ -250,6 +302,8 @@ struct yx_ctx {
   }
   // scratch
   DevBuf part_o, part_ml, counters, io_a, io_b, io_c, io_q;
+  DevBuf am_keys, am_counters;  // argmax: per-slice keys, per-row arrival counters
+  DevBuf mm_part, mm_counters;  // matmul: per-k-part output tiles, per-tile arrival counters
   // options
   long target_waves = 0;  // 0: one work item per CU
   int cus = 256;
@@ -275,8 +329,8 @@ struct yx_ctx {
   uint64_t epoch = 0, graph_epoch = 0, graph_gens = 0;
   uint64_t buffer_gens() const {
     uint64_t s = 0;
-    for (const DevBuf* b : {&d_pos, &d_slot, &d_pages, &part_o, &part_ml, &counters, &io_a, &io_b,
-                            &io_c, &io_q})
+    for (const DevBuf* b : {&d_meta, &d_pages, &part_o, &part_ml, &counters, &io_a, &io_b, &io_c,
+                            &io_q, &am_keys, &am_counters, &mm_part, &mm_counters})
       s += b->gen;
     return s;
   }
@@ -375,7 +429,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
         yx::PrefillItem w{};
         w.r0 = g.r0 + r;
         w.nrows = std::min(per, g.n - r);
-        w.pt_off = g.pt_off;
+        w.pt_off = g.dev_off;
         uint32_t lo = UINT32_MAX, hi = 0;
         for (uint32_t i = w.r0; i < w.r0 + w.nrows; ++i) {
           const uint32_t p = c->pos[i];
@@ -406,7 +460,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
   if (rows_per_sub == 0) return fail(YX_ERR_UNSUPPORTED, "more than 32 query heads per KV head");
 
   struct Sub {
-    uint32_t r0, n, pt_off, b0, b1;
+    uint32_t r0, n, pt_off, dev_off, b0, b1;
     int casc = -1;  // the shared prefix it belongs to
   };
   std::vector<Sub> subs;
@@ -417,6 +471,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
       s.r0 = g.r0 + r;
       s.n = std::min<uint32_t>(static_cast<uint32_t>(rows_per_sub), g.n - r);
       s.pt_off = g.pt_off;
+      s.dev_off = g.dev_off;
       uint32_t lo = UINT32_MAX, hi = 0;
       for (uint32_t i = s.r0; i < s.r0 + s.n; ++i) {
         uint32_t p = c->pos[i];
@@ -436,7 +491,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
   // kernel), instead of once per group. Only keys every row of the run sees (below
   // each row's position, no window cut) are shared; at least kMinShared blocks.
   struct Casc {
-    uint32_t r0, n, pt_off, blocks, first, count;
+    uint32_t r0, n, dev_off, blocks, first, count;
   };
   std::vector<Casc> cascs;
   const uint32_t bpp = static_cast<uint32_t>(page_size / 16);  // blocks per page
@@ -466,7 +521,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
         }
         blocks = std::min(blocks, pages_common * bpp);
         if (blocks >= kMinShared) {
-          Casc cc{subs[i].r0, rows, subs[i].pt_off, blocks, static_cast<uint32_t>(i),
+          Casc cc{subs[i].r0, rows, subs[i].dev_off, blocks, static_cast<uint32_t>(i),
                   static_cast<uint32_t>(j - i)};
           for (size_t k = i; k < j; ++k) {
             work -= blocks;  // read once below, not once per group
@@ -568,7 +623,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
       yx::AttnItem w{};
       w.r0 = cc.r0;
       w.nrows = cc.n;
-      w.pt_off = cc.pt_off;
+      w.pt_off = cc.dev_off;
       w.blk0 = 4 * static_cast<uint32_t>(static_cast<uint64_t>(nq) * ch / nch);
       w.blk1 = std::min(cc.blocks, 4 * static_cast<uint32_t>(static_cast<uint64_t>(nq) * (ch + 1) / nch));
       w.chunk = ch;
@@ -594,7 +649,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
       yx::AttnItem w{};
       w.r0 = s.r0;
       w.nrows = s.n;
-      w.pt_off = s.pt_off;
+      w.pt_off = s.dev_off;
       w.blk0 = s.b0 + 4 * static_cast<uint32_t>(static_cast<uint64_t>(nq) * ch / nch);
       w.blk1 = std::min(s.b1, s.b0 + 4 * static_cast<uint32_t>(static_cast<uint64_t>(nq) * (ch + 1) / nch));
       w.chunk = ch;
@@ -670,12 +725,14 @@ int upload_plan(yx_ctx* c, AttnPlan* p) {
   int rc = p->d_items.ensure(std::max<size_t>(ib, 16), c->stream);
   if (rc) return rc;
   if ((rc = c->staging[c->cur_staging].upload(p->d_items.p, items, ib, c->stream))) return rc;
+  p->dev_items = p->d_items.p;
   if (!p->members.empty()) {
     p->d_members = c->take_spare();
     if ((rc = p->d_members.ensure(p->members.size() * sizeof(yx::SubRef), c->stream))) return rc;
     rc = c->staging[c->cur_staging].upload(p->d_members.p, p->members.data(),
                                            p->members.size() * sizeof(yx::SubRef), c->stream);
     if (rc) return rc;
+    p->dev_members = p->d_members.p;
   }
   p->uploaded = true;
   return YX_OK;
@@ -707,6 +764,11 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   if (c->capturing && !c->plans.count(std::make_tuple(window, hq, hkv, kv->f32, kv->page)))
     return fail(YX_ERR_INVALID, "run the call once before capturing it (its work list is uploaded then)");
   if ((rc = build_plan(c, window, hq, hkv, kv->f32, kv->page, &plan))) return rc;
+  {
+    const auto key = std::make_tuple(window, hq, hkv, kv->f32, kv->page);
+    if (std::find(c->used_keys.begin(), c->used_keys.end(), key) == c->used_keys.end())
+      c->used_keys.push_back(key);
+  }
   // Logical rows per partial slot: the kernel's tile rows.
   const size_t rps = plan->wide ? static_cast<size_t>((plan->nt + 1) / 2) * 16 : static_cast<size_t>(plan->nt) * 8;
   const size_t po_need = plan->slots * hkv * rps * 128 * 4, pml_need = plan->slots * hkv * rps * 8;
@@ -745,8 +807,8 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     if ((rc = c->part_o.ensure(std::max<size_t>(1, po_need), c->stream))) return rc;
     if ((rc = c->part_ml.ensure(std::max<size_t>(1, pml_need), c->stream))) return rc;
     if ((rc = c->counters.ensure(std::max<size_t>(1, cnt_need), c->stream, true))) return rc;
-    d_items = plan->d_items.p;
-    d_members = plan->members.empty() ? nullptr : static_cast<const yx::SubRef*>(plan->d_members.p);
+    d_items = plan->dev_items;
+    d_members = plan->members.empty() ? nullptr : static_cast<const yx::SubRef*>(plan->dev_members);
     po = static_cast<float*>(c->part_o.p);
     pml = static_cast<float2*>(c->part_ml.p);
     cnt = static_cast<uint32_t*>(c->counters.p);
@@ -778,14 +840,14 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     if (qkv)
       hipLaunchKernelGGL((yx::paged_attn_prefill<true>), pgrid, dim3(64 * yx::kPrefillWaves), 0, c->stream,
                        static_cast<const yx::PrefillItem*>(d_items),
-                       static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_pages.p),
+                       c->dev_pos, static_cast<const uint32_t*>(c->d_pages.p),
                        kv->k[layer], kv->v[layer], q, out, static_cast<uint32_t>(hq),
                        static_cast<uint32_t>(hkv), shift, static_cast<uint32_t>(window),
                        scale * yx::kLog2e, *qkv);
     else
       hipLaunchKernelGGL((yx::paged_attn_prefill<false>), pgrid, dim3(64 * yx::kPrefillWaves), 0, c->stream,
                        static_cast<const yx::PrefillItem*>(d_items),
-                       static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_pages.p),
+                       c->dev_pos, static_cast<const uint32_t*>(c->d_pages.p),
                        kv->k[layer], kv->v[layer], q, out, static_cast<uint32_t>(hq),
                        static_cast<uint32_t>(hkv), shift, static_cast<uint32_t>(window),
                        scale * yx::kLog2e, yx::QkvIn{});
@@ -801,7 +863,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   hipEvent_t e0;
   if ((rc = prof_begin(c, YX_KERNEL_ATTENTION, &e0))) return rc;
   const auto* items = static_cast<const yx::AttnItem*>(d_items);
-  const auto* pos = static_cast<const uint32_t*>(c->d_pos.p);
+  const auto* pos = c->dev_pos;
   const auto* pages = static_cast<const uint32_t*>(c->d_pages.p);
   const uint32_t H = static_cast<uint32_t>(hq), HK = static_cast<uint32_t>(hkv);
   uint32_t P = 0;
@@ -814,18 +876,18 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   hipLaunchKernelGGL(yx::paged_attn_decode<NT>, grid, dim3(64 * yx::DecodeWaves<NT>::value), 0,      \
                      c->stream, items, pos, pages,                                                  \
                      kv->k[layer], kv->v[layer], q, out, po, pml, cnt, knew, vnew,                 \
-                     static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],       \
+                     c->dev_slot, kv->k[layer], kv->v[layer],       \
                      po_bytes, pml_bytes, H, HK, P, W, scale_log2)
   if (plan->f32) {
     hipLaunchKernelGGL(yx::paged_attn_decode_f32, grid, dim3(64 * yx::kWideWaves), 0, c->stream,
                        items, pos, pages, kv->kf(layer), kv->vf(layer), q, out, po, pml, cnt, knew,
-                       vnew, static_cast<const uint32_t*>(c->d_slot.p), kv->kf(layer),
+                       vnew, c->dev_slot, kv->kf(layer),
                        kv->vf(layer), po_bytes, pml_bytes, H, HK, P, W, scale_log2, mem);
   } else if (plan->balanced && !plan->wide) {
 #define YX_LAUNCH_BAL(QKV, UB, KN, VN, IN)                                                          \
   hipLaunchKernelGGL((yx::paged_attn_decode_balanced<QKV, UB>), grid, dim3(64 * yx::kBalWaves), 0,  \
                      c->stream, items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml,     \
-                     cnt, KN, VN, static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer],        \
+                     cnt, KN, VN, c->dev_slot, kv->k[layer],        \
                      kv->v[layer], po_bytes, pml_bytes, H, HK, P, W, scale_log2, IN)
     if (qkv && plan->small_units) YX_LAUNCH_BAL(true, 2, nullptr, nullptr, *qkv);
     else if (qkv) YX_LAUNCH_BAL(true, 4, nullptr, nullptr, *qkv);
@@ -836,7 +898,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
 #define YX_LAUNCH_WIDE(NT, QKV, KN, VN, IN, CASC)                                                   \
   hipLaunchKernelGGL((yx::paged_attn_decode_wide<NT, QKV, CASC>), grid, dim3(64 * yx::kWideWaves), 0, \
                      c->stream, items, pos, pages, kv->k[layer], kv->v[layer], q, out, po, pml,     \
-                     cnt, KN, VN, static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer],        \
+                     cnt, KN, VN, c->dev_slot, kv->k[layer],        \
                      kv->v[layer], po_bytes, pml_bytes, H, HK, P, W, scale_log2, IN, mem)
     const bool casc = plan->cascades > 0;  // shared prefixes only in one-tile passes
     if (qkv && casc) YX_LAUNCH_WIDE(1, true, nullptr, nullptr, *qkv, true);
@@ -867,12 +929,12 @@ int append_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* k, const float*
   if (kv->f32) {
     dim3 grid32(static_cast<unsigned>((threads * 2 + 255) / 256), 2);
     hipLaunchKernelGGL(yx::kv_append_f32, grid32, dim3(256), 0, c->stream, k, v,
-                       static_cast<const uint32_t*>(c->d_slot.p), kv->kf(layer), kv->vf(layer),
+                       c->dev_slot, kv->kf(layer), kv->vf(layer),
                        static_cast<uint32_t>(c->rows), static_cast<uint32_t>(kv->hkv),
                        static_cast<uint32_t>(kv->page));
   } else {
     hipLaunchKernelGGL(yx::kv_append_f16, grid, dim3(256), 0, c->stream, k, v,
-                       static_cast<const uint32_t*>(c->d_slot.p), kv->k[layer], kv->v[layer],
+                       c->dev_slot, kv->k[layer], kv->v[layer],
                        static_cast<uint32_t>(c->rows), static_cast<uint32_t>(kv->hkv),
                        static_cast<uint32_t>(kv->page));
   }
@@ -906,14 +968,14 @@ int qk_rope_impl(yx_ctx* c, yx_kv* kv, size_t layer, const yx::QkvIn& in, size_t
   if (kv->f32)
     hipLaunchKernelGGL(yx::qk_norm_rope_append<float>, grid, dim3(yx::kRopeThreads), 0, c->stream,
                        in.qkv, in.q_norm, in.k_norm, in.rope_cs, in.rope_len, in.eps,
-                       static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_slot.p),
+                       c->dev_pos, c->dev_slot,
                        kv->kf(layer), kv->vf(layer), q_out, static_cast<uint32_t>(hq),
                        static_cast<uint32_t>(hkv), page_shift, static_cast<uint32_t>(nvec),
                        static_cast<uint32_t>(kv_only ? hq : 0));
   else
     hipLaunchKernelGGL(yx::qk_norm_rope_append<_Float16>, grid, dim3(yx::kRopeThreads), 0, c->stream,
                        in.qkv, in.q_norm, in.k_norm, in.rope_cs, in.rope_len, in.eps,
-                       static_cast<const uint32_t*>(c->d_pos.p), static_cast<const uint32_t*>(c->d_slot.p),
+                       c->dev_pos, c->dev_slot,
                        kv->k[layer], kv->v[layer], q_out, static_cast<uint32_t>(hq),
                        static_cast<uint32_t>(hkv), page_shift, static_cast<uint32_t>(nvec),
                        static_cast<uint32_t>(kv_only ? hq : 0));
@@ -975,7 +1037,8 @@ int yx_ctx_destroy(yx_ctx* c) {
   }
   for (DevBuf& b : c->spare) b.release();
   c->spare.clear();
-  for (DevBuf* b : {&c->d_pos, &c->d_slot, &c->d_pages, &c->part_o, &c->part_ml, &c->counters,
+  for (DevBuf* b : {&c->d_meta, &c->d_pages, &c->am_keys, &c->am_counters, &c->mm_part, &c->mm_counters,
+                    &c->part_o, &c->part_ml, &c->counters,
                     &c->io_a, &c->io_b, &c->io_c, &c->io_q})
     b->release();
   if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
@@ -1234,18 +1297,136 @@ int yx_pass_begin(yx_ctx* c, size_t rows, const uint32_t* pos, const uint32_t* k
     if (!c->groups.empty() && c->groups.back().pt_off == pt_off[i])
       c->groups.back().n += 1;
     else
-      c->groups.push_back(Group{static_cast<uint32_t>(i), 1, pt_off[i]});
+      c->groups.push_back(Group{static_cast<uint32_t>(i), 1, pt_off[i], 0});
   }
   c->cur_staging ^= 1;
   Staging& st = c->staging[c->cur_staging];
   if ((rc = st.reset())) return rc;
-  if ((rc = c->d_pos.ensure(std::max<size_t>(4, rows * 4), c->stream))) return rc;
-  if ((rc = c->d_slot.ensure(std::max<size_t>(4, rows * 4), c->stream))) return rc;
-  if ((rc = c->d_pages.ensure(std::max<size_t>(4, npages * 4), c->stream))) return rc;
-  if ((rc = st.upload(c->d_pos.p, pos, rows * 4, c->stream))) return rc;
-  if ((rc = st.upload(c->d_slot.p, kv_slot, rows * 4, c->stream))) return rc;
-  if ((rc = st.upload(c->d_pages.p, pages, npages * 4, c->stream))) return rc;
+
+  // Page tables on the device: one region per group, entries [0, need) of the group's
+  // table. A table runs to the next group's offset (or the end of the pass's tables) and
+  // at least as far as the group's positions reach with the smallest page size, since a
+  // table is followed by later ones (PassMeta::page_table). The previous pass's regions
+  // are kept when there are as many groups and each fits its region; the regions are
+  // then updated in place, entry runs that differ from what the device holds.
+  const size_t ng = c->groups.size();
+  std::vector<uint32_t> starts(pt_off, pt_off + rows);
+  std::sort(starts.begin(), starts.end());
+  starts.erase(std::unique(starts.begin(), starts.end()), starts.end());
+  std::vector<uint32_t> need(ng);
+  bool keep = c->region_off.size() == ng;
+  for (size_t g = 0; g < ng; ++g) {
+    const Group& gr = c->groups[g];
+    auto nx = std::upper_bound(starts.begin(), starts.end(), gr.pt_off);
+    const uint32_t len = (nx == starts.end() ? static_cast<uint32_t>(npages) : *nx) - gr.pt_off;
+    uint32_t reach = 0;
+    for (uint32_t r = gr.r0; r < gr.r0 + gr.n; ++r) reach = std::max(reach, pos[r] / 16 + 1);
+    need[g] = std::min(static_cast<uint32_t>(npages) - gr.pt_off, std::max(len, reach));
+    if (keep && need[g] > c->region_cap[g]) keep = false;
+  }
+  if (!keep) {
+    size_t total = 0;
+    c->region_off.assign(ng, 0);
+    c->region_cap.assign(ng, 0);
+    for (size_t g = 0; g < ng; ++g) {
+      const size_t cap = (need[g] + std::max<size_t>(64, need[g] / 8) + 63) / 64 * 64;
+      if (total + cap > 0x7fffffff) return fail(YX_ERR_INVALID, "pass too large");
+      c->region_off[g] = static_cast<uint32_t>(total);
+      c->region_cap[g] = static_cast<uint32_t>(cap);
+      total += cap;
+    }
+    if ((rc = c->d_pages.ensure(std::max<size_t>(4, total * 4), c->stream))) return rc;
+    c->dev_mirror.assign(total, 0xffffffffu);  // matches no page id: every entry is sent
+  }
+  std::vector<uint32_t> runs, data;  // runs of (device index, count, data index)
+  for (size_t g = 0; g < ng; ++g) {
+    c->groups[g].dev_off = c->region_off[g];
+    const uint32_t* src = pages + c->groups[g].pt_off;
+    uint32_t* mir = c->dev_mirror.data() + c->region_off[g];
+    for (uint32_t j = 0; j < need[g]; ++j) {
+      if (mir[j] == src[j]) continue;
+      const uint32_t d = c->region_off[g] + j;
+      if (!runs.empty() && runs[runs.size() - 3] + runs[runs.size() - 2] == d)
+        ++runs[runs.size() - 2];
+      else
+        runs.insert(runs.end(), {d, 1u, static_cast<uint32_t>(data.size())});
+      data.push_back(src[j]);
+      mir[j] = src[j];
+    }
+  }
+  const uint32_t nruns = static_cast<uint32_t>(runs.size() / 3);
+  c->pages_sent += data.size();
+  c->runs_sent += nruns;
+
+  // The work lists of the attention calls the previous pass made are built now and go
+  // in the same copy (a decode loop calls the same layers every step); other calls
+  // build theirs at their first use.
+  std::vector<AttnPlan*> pre;
+  {
+    auto keys = std::move(c->used_keys);
+    c->used_keys.clear();
+    for (const auto& k : keys) {
+      AttnPlan* p = nullptr;
+      if (build_plan(c, std::get<0>(k), std::get<1>(k), std::get<2>(k), std::get<3>(k), std::get<4>(k), &p) == YX_OK)
+        pre.push_back(p);
+    }
+  }
+
+  // One copy: positions, slots, page-table runs and data, prebuilt work lists.
+  auto r256 = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
+  size_t off = 0;
+  auto take = [&](size_t b) {
+    const size_t o = off;
+    off += r256(b);
+    return o;
+  };
+  const size_t o_pos = take(rows * 4), o_slot = take(rows * 4), o_runs = take(runs.size() * 4),
+               o_data = take(data.size() * 4);
+  std::vector<std::pair<size_t, size_t>> o_plan;
+  for (AttnPlan* p : pre) {
+    const size_t oi = take(p->item_bytes());
+    o_plan.emplace_back(oi, take(p->members.size() * sizeof(yx::SubRef)));
+  }
+  const size_t total = std::max<size_t>(off, 256);
+  if ((rc = c->d_meta.ensure(total, c->stream))) return rc;
+  char* h = nullptr;
+  if ((rc = st.reserve(total, &h))) return rc;
+  std::memcpy(h + o_pos, pos, rows * 4);
+  std::memcpy(h + o_slot, kv_slot, rows * 4);
+  if (!runs.empty()) std::memcpy(h + o_runs, runs.data(), runs.size() * 4);
+  if (!data.empty()) std::memcpy(h + o_data, data.data(), data.size() * 4);
+  char* dm = static_cast<char*>(c->d_meta.p);
+  for (size_t i = 0; i < pre.size(); ++i) {
+    AttnPlan* p = pre[i];
+    const void* items = p->prefill ? static_cast<const void*>(p->pitems.data()) : p->items.data();
+    if (p->item_bytes()) std::memcpy(h + o_plan[i].first, items, p->item_bytes());
+    if (!p->members.empty())
+      std::memcpy(h + o_plan[i].second, p->members.data(), p->members.size() * sizeof(yx::SubRef));
+    p->dev_items = dm + o_plan[i].first;
+    p->dev_members = dm + o_plan[i].second;
+    p->uploaded = true;
+  }
+  if ((rc = st.send(c->d_meta.p, off, c->stream))) return rc;
+  c->dev_pos = reinterpret_cast<const uint32_t*>(dm + o_pos);
+  c->dev_slot = reinterpret_cast<const uint32_t*>(dm + o_slot);
+  if (nruns) {
+    hipLaunchKernelGGL(page_runs_apply, dim3(std::min<uint32_t>(nruns, 256)), dim3(256), 0, c->stream,
+                       reinterpret_cast<const uint32_t*>(dm + o_runs), nruns,
+                       reinterpret_cast<const uint32_t*>(dm + o_data), static_cast<uint32_t*>(c->d_pages.p));
+    YX_HIP(hipGetLastError());
+  }
   c->have_pass = true;
+  return YX_OK;
+}
+
+int yx_ctx_get_stat(yx_ctx* c, const char* key, uint64_t* out) {
+  if (!c || !key || !out) return fail(YX_ERR_INVALID, "null argument");
+  if (!std::strcmp(key, "page_entries_sent"))
+    *out = c->pages_sent;
+  else if (!std::strcmp(key, "page_runs_sent"))
+    *out = c->runs_sent;
+  else
+    return fail(YX_ERR_INVALID, std::string("unknown statistic ") + key);
   return YX_OK;
 }
 
@@ -1437,6 +1618,65 @@ int yx_dev_checksum(yx_ctx* c, const void* src, size_t bytes, uint64_t* out) {
   YX_HIP(hipGetLastError());
   YX_HIP(hipMemcpyAsync(out, c->io_c.p, 8, hipMemcpyDeviceToHost, c->stream));
   YX_HIP(hipStreamSynchronize(c->stream));
+  return YX_OK;
+}
+
+int yx_matmul_bf16_dev(yx_ctx* c, const float* x, const uint16_t* w, float* out, size_t t,
+                       size_t k, size_t n) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  if (t == 0 || n == 0) return YX_OK;
+  if (!x || !w || !out) return fail(YX_ERR_INVALID, "null x, w or out");
+  if (k == 0 || k % 8) return fail(YX_ERR_UNSUPPORTED, "k must be a positive multiple of 8");
+  if (t > 0xffffffffu || k > 0xffffffffu || n > 0xffffffffu || (n + 15) / 16 > 0x7fffffff ||
+      (t + 15) / 16 > 0xffff)
+    return fail(YX_ERR_UNSUPPORTED, "matmul dimensions too large");
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w) % 16)
+    return fail(YX_ERR_INVALID, "x and w must be 16-byte aligned");
+  int rc = c->set_device();
+  if (rc) return rc;
+  // Workgroups per output tile along k: about two workgroups per CU in all, each wave
+  // at least one pass of its loop (kMmSteps steps of 32).
+  const size_t tiles = ((n + 15) / 16) * ((t + 15) / 16), steps = (k + 31) / 32;
+  const size_t ks = std::max<size_t>(1, std::min<size_t>({(2 * static_cast<size_t>(c->cus) + tiles - 1) / tiles,
+                                                           steps / (yx::kMmWaves * yx::kMmSteps), 64}));
+  if (ks > 1) {
+    if (c->capturing && (c->mm_part.cap < tiles * ks * 1024 || c->mm_counters.cap < tiles * 4))
+      return fail(YX_ERR_INVALID, "run the call once before capturing it (its scratch is allocated then)");
+    if (tiles * ks * 1024 > 0xffffffffu) return fail(YX_ERR_UNSUPPORTED, "matmul dimensions too large");
+    if ((rc = c->mm_part.ensure(tiles * ks * 1024, c->stream))) return rc;
+    if ((rc = c->mm_counters.ensure(tiles * 4, c->stream, true))) return rc;
+  }
+  hipLaunchKernelGGL(yx::matmul_bf16_rows,
+                     dim3(static_cast<unsigned>((n + 15) / 16), static_cast<unsigned>((t + 15) / 16),
+                          static_cast<unsigned>(ks)),
+                     dim3(64 * yx::kMmWaves), 0, c->stream, x, w, out, static_cast<uint32_t>(t),
+                     static_cast<uint32_t>(k), static_cast<uint32_t>(n),
+                     static_cast<yx::f32x4*>(c->mm_part.p), static_cast<uint32_t>(c->mm_part.cap),
+                     static_cast<uint32_t*>(c->mm_counters.p));
+  YX_HIP(hipGetLastError());
+  return YX_OK;
+}
+
+int yx_argmax_rows_dev(yx_ctx* c, const float* logits, size_t rows, size_t cols, uint32_t* out) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  if (rows == 0) return YX_OK;
+  if (!logits || !out) return fail(YX_ERR_INVALID, "null logits or out");
+  if (cols == 0) return fail(YX_ERR_INVALID, "empty rows");
+  if (rows > 0xffff || cols > 0x7fffffff) return fail(YX_ERR_UNSUPPORTED, "argmax dimensions too large");
+  int rc = c->set_device();
+  if (rc) return rc;
+  // Slices per row: each thread's share of a slice in one pass of its loads
+  // (kArgmaxQuads quads), so a slice takes one round trip to memory.
+  const size_t per_slice = static_cast<size_t>(yx::kArgmaxThreads) * yx::kArgmaxQuads * 4;
+  const size_t nsl = std::max<size_t>(1, std::min<size_t>((cols + per_slice - 1) / per_slice, 1024));
+  if (c->capturing && (c->am_keys.cap < rows * nsl * 8 || c->am_counters.cap < rows * 4))
+    return fail(YX_ERR_INVALID, "run the call once before capturing it (its scratch is allocated then)");
+  if ((rc = c->am_keys.ensure(rows * nsl * 8, c->stream))) return rc;
+  if ((rc = c->am_counters.ensure(rows * 4, c->stream, true))) return rc;
+  hipLaunchKernelGGL(yx::argmax_rows, dim3(static_cast<unsigned>(nsl), static_cast<unsigned>(rows)),
+                     dim3(yx::kArgmaxThreads), 0, c->stream, logits, static_cast<uint32_t>(cols), out,
+                     static_cast<unsigned long long*>(c->am_keys.p), static_cast<uint32_t*>(c->am_counters.p));
+  YX_HIP(hipGetLastError());
   return YX_OK;
 }
 
