@@ -606,6 +606,8 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
     const Casc& cc = cascs[ci];
     const uint32_t nq = (cc.blocks + 3) / 4;
     const uint32_t cq = chunk_quads(nq, cb);
+    if (cq * 4 > 64 * waves)  // each wave's page ids fit its 64 lanes
+      return fail(YX_ERR_UNSUPPORTED, "shared prefix too long for 256 chunks of the widest work item");
     const uint32_t nch = (nq + cq - 1) / cq;
     casc_base[ci] = static_cast<uint32_t>(slot);
     casc_nch[ci] = nch;
