@@ -126,3 +126,30 @@ def test_shared_prefix_f32_arena(hip):
     got = hip.attend(sc.kv, 0, q, hq)
     exact = sc.orc[0].attend_f64(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
     assert np.abs(got - exact).max() < 1e-5
+
+
+@pytest.mark.parametrize("cut", [1, 7, 14])
+def test_shared_prefix_window_cutting_inside_the_first_block(hip, cut):
+    """A window that leaves every row's first visible key inside block 0 (1-15 keys cut):
+    the rows still start at block 0, so the shared prefix is attended once for all of
+    them, and each row's window mask applies inside the shared blocks. The rows' positions
+    differ by at most one, so every row's cut stays within 1-15."""
+    hq, hkv = 16, 4
+    sc = Scenario(hip, pages=700, page=16, hkv=hkv, pool_seed=35)
+    _, seqs = _forks(sc, 2000, [40, 41, 40, 41])
+    pr = sc.run_pass([(s, 1) for s in seqs])
+    sc.store(pr)
+    rows = len(pr.meta.pos)
+    pos = np.asarray(pr.meta.pos)
+    window = int(pos.min()) + 1 - cut  # the earliest row sees keys from `cut` on
+    assert all(0 < p + 1 - window < 16 for p in pos)
+    q = sc.draw(rows * hq * D).reshape(rows, hq * D)
+    got = hip.attend(sc.kv, 0, q, hq, window=window)
+    with _option(hip, "attn_cascade", 0):
+        plain = hip.attend(sc.kv, 0, q, hq, window=window)
+    want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
+    for name, a in (("cascade", got), ("plain", plain)):
+        assert close(a, want).all(), f"{name}: max abs err {np.abs(a - want).max()}"
+    # The window matters: attention over the whole prefix differs.
+    full = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
+    assert np.abs(full - want).max() > 1e-6
