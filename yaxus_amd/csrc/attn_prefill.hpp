@@ -24,9 +24,17 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "attn_decode.hpp"
 
 namespace yx {
+
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef __fp16 fp16x4_raw __attribute__((__vector_size__(8)));  // the builtin's operand type
+typedef __attribute__((address_space(3))) fp16x4_raw lds_half4;
 
 struct PrefillItem {
   uint32_t r0;      // first pass row of the tile
@@ -93,28 +101,40 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
   const uint32_t* pt = pages + it.pt_off;
   // Each wave moves an eighth of a stage: wave w takes block w / 2 of the stage, its K
   // (w even) or V (w odd), as four 1 KiB rows. K row p is read transposed ([p][key][g] in
-  // the arena, [p][g][key] in LDS): lane l fetches key l % 16, dims group l / 16.
+  // the arena, [p][g][key] in LDS): lane l fetches key l % 16, dims group l / 16. V keeps
+  // its [key][128] rows, but the 32-byte chunks of key k's row are stored XOR-swizzled
+  // (chunk j at j ^ (k & 7)) so that the transposing reads below stay at the minimum of
+  // two passes per 512 bytes; within a 1 KiB row lane l lands on key 4r + l / 16, piece
+  // l % 16, and so fetches the piece that belongs there.
   static_assert(kPrefillWaves == 8 && SB == 4, "the stage split below assumes 8 waves, 4 blocks");
   constexpr int kRowsPerWave = 4;  // 1 KiB rows (loads) per wave per stage
   const uint32_t my_blk = static_cast<uint32_t>(wave >> 1);
   const bool my_v = (wave & 1) != 0;
-  const uint32_t my_row0 = 0;
-  const uint32_t lane_src = my_v ? static_cast<uint32_t>(lane) * 16u
-                                 : static_cast<uint32_t>((lane & 15) * 4 + (lane >> 4)) * 16u;
+  uint32_t lane_src[kRowsPerWave];
+#pragma unroll
+  for (int r = 0; r < kRowsPerWave; ++r) {
+    const uint32_t key = 4 * r + (lane >> 4), pp = lane & 15;
+    lane_src[r] = my_v ? key * 256u + (2u * ((pp >> 1) ^ (key & 7u)) + (pp & 1u)) * 16u
+                       : static_cast<uint32_t>(r * 1024 + ((lane & 15) * 4 + (lane >> 4)) * 16);
+  }
   const char* my_arena = reinterpret_cast<const char*>(my_v ? vc : kc);
   const uint32_t ring_base = static_cast<uint32_t>(
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) half8*)&ring[0][0]));
-  auto issue = [&](uint32_t st, uint32_t slot) {  // stage st into ring slot `slot`
+  // The page of the block a wave moves for stage st is read one stage ahead, so the
+  // scalar load's latency is not waited for right after the stage's barrier.
+  auto page_of = [&](uint32_t st) {
     uint32_t b = it.blk0 + st * SB + my_blk;
     b = b < it.blk1 ? b : it.blk1 - 1;  // past the end: re-read the last block (unused)
-    const uint32_t page = pt[b >> bpp_shift];
-    const char* blk = my_arena + ((static_cast<size_t>(page) * hkv + kh) * head_stride +
-                                  static_cast<size_t>(b & bpp_mask) * 16 * kD) * 2;
+    return pt[b >> bpp_shift] * hkv * head_stride + static_cast<size_t>(b & bpp_mask) * 16 * kD;
+  };
+  size_t next_elem = page_of(0);
+  auto issue = [&](uint32_t st, uint32_t slot) {  // stage st into ring slot `slot`
+    const char* blk = my_arena + (next_elem + kh * head_stride) * 2;
+    next_elem = page_of(st + 1);
     const uint32_t dst = ring_base + slot * (2 * SB * 256 * 16) +
                          (my_v ? SB * 4096u : 0u) + my_blk * 4096u;
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r)
-      load_to_lds16(blk + (my_row0 + r) * 1024 + lane_src, dst + (my_row0 + r) * 1024);
+    for (int r = 0; r < kRowsPerWave; ++r) load_to_lds16(blk + lane_src[r], dst + r * 1024);
   };
   // q and pos are read first, unconditionally (rows past the tile read row 0 and are
   // zeroed), so that waiting for them does not wait for the K/V stages issued after.
@@ -235,161 +255,282 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
     wlo = min(wlo, __builtin_amdgcn_readfirstlane(lo));
   }
 
-  float m[NT], l[NT];
-  floatx4 acc[NT][8];
+  static_assert(NT == 1, "the pipelined loop below takes one MFMA tile per wave");
+  float m = -INFINITY;
+  float lsum = 0.0f;  // this lane's share of its column's sum (its 8 keys of every pair)
+  floatx4 acc[8];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    m[t] = -INFINITY;
-    l[t] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[t][j] = floatx4{0, 0, 0, 0};
-  }
+  for (int j = 0; j < 8; ++j) acc[j] = floatx4{0, 0, 0, 0};
   const int key_end = static_cast<int>(it.blk1 * 16);
+  const int first_key = static_cast<int>(it.blk0 * 16);
+  const int npair = static_cast<int>(2 * nst);
+  // Pair i holds keys first_key + 32 i .. + 31. This wave computes the pairs [pa, pb) that
+  // hold a key some column of the wave can see; the others it only passes through.
+  int pa = npair, pb = npair;
+  if (wmax >= 0) {
+    const int d = wlo - first_key;
+    pa = d <= 0 ? 0 : d / 32;
+    const int e = min(wmax, key_end - 1) - first_key;
+    pb = e < 0 ? 0 : min(npair, e / 32 + 1);
+  }
 
-  auto compute = [&](const half8* kbuf, const half8* vbuf, uint32_t s0) {
-    // Two blocks (32 keys) per softmax update; PV as 16x16x32 products over both.
+  // Per lane, the byte offset of its transposing-read address for dim group j within a
+  // block of V (see the swizzle above): key k = 4 g + c / 4, dims 16 j + 4 (c % 4).
+  uint32_t vtr_off[8];
 #pragma unroll
-    for (int pr2 = 0; pr2 < SB / 2; ++pr2) {
-      const int key0 = static_cast<int>((s0 + 2 * pr2) * 16);
-      if (key0 > wmax || key0 + 31 < wlo || key0 >= key_end) continue;  // uniform
-      half8 kk[2][4], vv[2][4];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int base = (2 * pr2 + h) * 256;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) kk[h][p] = kbuf[base + p * 64 + lane];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) vv[h][i] = vbuf[base + (4 * g + i) * 16 + c];
-      }
-      // Scores of every (tile, block): 2 * NT accumulators, each taking the hi-part
-      // products for p = 0..3 and then the lo-part ones, so consecutive products into one
-      // accumulator are 2 * NT MFMAs apart and no add joins the parts afterwards.
-      floatx4 sc[NT][2];
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) sc[t][h] = floatx4{0, 0, 0, 0};
-#pragma unroll
-      for (int part = 0; part < 2; ++part)
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-#pragma unroll
-          for (int t = 0; t < NT; ++t)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-              sc[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk[h][p], part ? ql[t][p] : qh[t][p],
-                                                                sc[t][h], 0, 0, 0);
-      half8 ph[NT], pl[NT];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        // Every key of the pair visible to every row of the tile: no mask needed.
-        const bool whole = (key0 + 31 <= tmin[t]) & (key0 >= tlo[t]) & (key0 + 32 <= key_end);
-        float x[8], bmax = -INFINITY;
-        if (whole) {  // uniform: the common case needs no mask
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              x[h * 4 + i] = sc[t][h][i];
-              bmax = fmaxf(bmax, x[h * 4 + i]);
-            }
-        } else {
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int kp = key0 + h * 16 + 4 * g + i;
-              // Bitwise, not short-circuit: straight-line selects instead of branches.
-              const bool ok = (kp >= rlo[t]) & (kp <= rpos[t]) & (kp < key_end);
-              x[h * 4 + i] = ok ? sc[t][h][i] : -INFINITY;
-              bmax = fmaxf(bmax, x[h * 4 + i]);
-            }
-        }
-        bmax = max_xor32(max_xor16(bmax));
-        // The running maximum moves only when some column's maximum grew by more than
-        // kLazyRescale (or was still empty): between moves, scores may exceed it by up
-        // to that, so P stays below 2^kLazyRescale, well inside binary16 and f32. The
-        // result is the same softmax (the sum uses the same offset); most stages then
-        // skip the rescale of the accumulators.
-        const float mn = fmaxf(m[t], bmax);
-        if (__builtin_amdgcn_ballot_w64(mn > m[t] + kLazyRescale)) {  // wave-uniform
-          const float corr = mn != -INFINITY ? __builtin_amdgcn_exp2f(m[t] - mn) : 1.0f;
-          l[t] *= corr;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[t][j] *= corr;
-          m[t] = mn;
-        }
-        // A whole tile has a finite maximum by now; otherwise a column that has seen no
-        // key yet (maximum -inf) gets zeros.
-        const bool live = whole || m[t] != -INFINITY;
-        float pr[8], rs = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          pr[i] = live ? __builtin_amdgcn_exp2f(x[i] - m[t]) : 0.0f;
-          rs += pr[i];
-        }
-        rs = sum_xor32(sum_xor16(rs));
-        l[t] += rs;
-        // P as an f16 hi part plus an f16 lo part; element e of a lane is key
-        // (e / 4) * 16 + 4g + e % 4 of the pair, as the V operand below.
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          ph[t][e] = static_cast<_Float16>(pr[e]);
-          if constexpr (kPrefillSplitP) pl[t][e] = static_cast<_Float16>(pr[e] - static_cast<float>(ph[t][e]));
-        }
-      }
-      // PV: every (tile, dim group) hi product, then every lo product, so that the
-      // two products into one accumulator are 8 * NT MFMAs apart.
-      half8 va[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        va[j] = half8{vv[0][0][j], vv[0][1][j], vv[0][2][j], vv[0][3][j],
-                      vv[1][0][j], vv[1][1][j], vv[1][2][j], vv[1][3][j]};
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[j], ph[t], acc[t][j], 0, 0, 0);
-      if constexpr (kPrefillSplitP) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[j], pl[t], acc[t][j], 0, 0, 0);
-      }
-    }
-  };
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t k = 4u * g + (c >> 2);
+    vtr_off[j] = k * 256u + 32u * (static_cast<uint32_t>(j) ^ (k & 7u)) + 8u * (c & 3);
+  }
 
-  uint32_t slot = 0;
-  for (uint32_t st = 0; st < nst; ++st) {
-    // This wave's loads of stage st are done when at most the kRing - 2 later stages'
-    // (kRowsPerWave loads each) are in flight; the barrier then makes every wave's part visible,
-    // and every wave has finished the stage before (whose slot is refilled next).
-    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(kRowsPerWave * (kRing - 2)) : "memory");
+  // Stage st becomes readable: this wave's loads of it are done when at most the
+  // kRing - 2 later stages' are in flight, and the barrier makes every wave's part
+  // visible. Every wave has then also issued and (lgkmcnt) finished its reads of the
+  // stage before st, whose slot is refilled with stage st + kRing - 1.
+  auto stage_enter = [&](uint32_t st) {
+    __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)" ::"n"(kRowsPerWave * (kRing - 2))
+                     : "memory");
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
-    issue(st + kRing - 1, slot == 0 ? kRing - 1 : slot - 1);
-    compute(&ring[slot][0], &ring[slot][SB * 256], it.blk0 + st * SB);
-    slot = slot + 1 == kRing ? 0 : slot + 1;
+    issue(st + kRing - 1, (st + kRing - 1) & (kRing - 1));
+  };
+  auto pair_lds = [&](int i) {  // LDS byte address of pair i's K (its V is 16 KiB on)
+    return ring_base + ((static_cast<uint32_t>(i) >> 1) & (kRing - 1)) * (2 * SB * 256 * 16) +
+           (static_cast<uint32_t>(i) & 1u) * 8192u;
+  };
+  // S^T of pair i: 2 accumulators (one per block), each taking the hi-part products for
+  // p = 0..3 and then the lo-part ones, 2 MFMAs apart.
+  auto qk = [&](int i, floatx4 (&sc)[2]) {
+    const half8* kb = reinterpret_cast<const half8*>(
+        reinterpret_cast<const char*>(&ring[0][0]) + (pair_lds(i) - ring_base));
+    half8 kk[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int p = 0; p < 4; ++p) kk[h][p] = kb[h * 256 + p * 64 + lane];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) sc[h] = floatx4{0, 0, 0, 0};
+#pragma unroll
+    for (int part = 0; part < 2; ++part)
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk[h][p], part ? ql[0][p] : qh[0][p], sc[h], 0, 0, 0);
+  };
+  // V^T operand of dim group j: row c is dim 16 j + c, element e is key
+  // (e / 4) * 16 + 4 g + e % 4 of the pair (the order of P). Each half is one transposing
+  // read: in a 16-lane group, lane i receives element i % 4 of the 8 bytes source lane
+  // 4 e + i / 4 addressed, so source lane s (= c) addresses key 4 g + s / 4, dims
+  // 16 j + 4 (s % 4) .. + 3, at its swizzled place.
+  auto read_v = [&](int i, half8 (&va)[8]) {
+    const uint32_t vb = pair_lds(i) + SB * 4096u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const lds_half4* p0 = reinterpret_cast<const lds_half4*>(
+          reinterpret_cast<const __attribute__((address_space(3))) char*>(static_cast<uintptr_t>(vb)) + vtr_off[j]);
+      const half4 lo = __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(const_cast<lds_half4*>(p0)));
+      const half4 hi = __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(const_cast<lds_half4*>(p0 + 512)));
+      va[j] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+  };
+  // Online softmax of pair i for the wave's columns, in two parts. The running maximum
+  // moves only when some column's maximum grew by more than kLazyRescale (or was still
+  // empty): between moves, scores may exceed it by up to that, so P stays below
+  // 2^kLazyRescale, well inside binary16 and f32; the sum uses the same offset, so the
+  // softmax is the same. Part one masks the scores, finds the maxima and, when the
+  // maximum moves (wave-uniform, rare after the first pairs), rescales the accumulators
+  // and the sum in place.
+  auto rescale = [&](auto masked, int i, const floatx4 (&sc)[2], float (&x)[8]) {
+    const int key0 = first_key + 32 * i;
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        if constexpr (decltype(masked)::value) {
+          const int kp = key0 + h * 16 + 4 * g + ii;
+          // Bitwise, not short-circuit: straight-line selects instead of branches.
+          const bool ok = (kp >= rlo[0]) & (kp <= rpos[0]) & (kp < key_end);
+          x[h * 4 + ii] = ok ? sc[h][ii] : -INFINITY;
+        } else {
+          x[h * 4 + ii] = sc[h][ii];
+        }
+        bmax = fmaxf(bmax, x[h * 4 + ii]);
+      }
+    bmax = max_xor32(max_xor16(bmax));
+    const float mn = fmaxf(m, bmax);
+    if (__builtin_amdgcn_ballot_w64(mn > m + kLazyRescale)) {  // wave-uniform
+      // A column still empty after this pair (mn = -inf) keeps its (zero) state.
+      const float corr = mn != -INFINITY ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
+      lsum *= corr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] *= corr;
+      m = mn;
+    }
+  };
+  // Part two: P as f16 hi + lo parts (element e of a lane is key (e / 4) * 16 + 4 g + e % 4
+  // of the pair) and this lane's share of the sum. Unmasked pairs are whole for every
+  // column, so m is finite there; a masked column that has seen no key yet (m = -inf)
+  // gets zeros.
+  auto probs = [&](auto masked, const float (&x)[8], half8& ph, half8& pl) {
+    float pr[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if constexpr (decltype(masked)::value)
+        pr[e] = m != -INFINITY ? __builtin_amdgcn_exp2f(x[e] - m) : 0.0f;
+      else
+        pr[e] = __builtin_amdgcn_exp2f(x[e] - m);
+    }
+    float rs = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) rs += pr[e];
+    lsum += rs;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ph[e] = static_cast<_Float16>(pr[e]);
+      if constexpr (kPrefillSplitP) pl[e] = static_cast<_Float16>(pr[e] - static_cast<float>(ph[e]));
+    }
+  };
+  // O^T += V^T P^T: every dim group's hi product, then every lo product (the two products
+  // into one accumulator 8 MFMAs apart).
+  auto pv = [&](const half8 (&va)[8], const half8& ph, const half8& pl) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[j], ph, acc[j], 0, 0, 0);
+    if constexpr (kPrefillSplitP) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[j], pl, acc[j], 0, 0, 0);
+    }
+  };
+  // One pair step, software-pipelined: this pair's V is read (LDS) while its maxima are
+  // found; the next pair's scores (16 MFMAs) are interleaved with this pair's
+  // exponentials (VALU) in one block; then this pair's products. The scores of pair i
+  // arrive in sc, and pair i + 1's leave in it. At the end of a stage (odd i) the next
+  // stage is entered between this pair's reads and the next pair's.
+  floatx4 sc[2];
+  auto step = [&](auto masked, auto has_next, int i) {
+    half8 va[8];
+    read_v(i, va);
+    float x[8];
+    rescale(masked, i, sc, x);
+    if ((i & 1) && (i >> 1) + 1 < static_cast<int>(nst)) stage_enter(static_cast<uint32_t>(i >> 1) + 1);
+    half8 ph, pl;
+    if constexpr (decltype(has_next)::value) {
+      // The next pair's K, then its 16 score MFMAs two at a time (one per block, so two
+      // independent chains), each couple followed by a slice of this pair's softmax. The
+      // sched_barrier fences keep this order: the matrix pipe runs the products while
+      // the vector pipe does the slices.
+      const half8* kb = reinterpret_cast<const half8*>(
+          reinterpret_cast<const char*>(&ring[0][0]) + (pair_lds(i + 1) - ring_base));
+      half8 kk[2][4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) kk[h][p] = kb[h * 256 + p * 64 + lane];
+      floatx4 scn[2] = {floatx4{0, 0, 0, 0}, floatx4{0, 0, 0, 0}};
+      float pr[8], rs = 0.0f;
+      floatx2 hf[4];  // ph as f32, pairwise
+      auto mm = [&](int k) {  // score MFMAs k (hi parts p = k, then lo parts p = k - 4)
+        const int p = k & 3;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          scn[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk[h][p], k < 4 ? qh[0][p] : ql[0][p], scn[h], 0, 0, 0);
+      };
+      auto ex = [&](int e) {
+        if constexpr (decltype(masked)::value)
+          pr[e] = m != -INFINITY ? __builtin_amdgcn_exp2f(x[e] - m) : 0.0f;
+        else
+          pr[e] = __builtin_amdgcn_exp2f(x[e] - m);
+      };
+      auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
+      ex(0); ex(1); ex(2); ex(3);
+      fence();
+      mm(0); ex(4); ex(5); ex(6); ex(7);
+      fence();
+      mm(1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const half2_t h2 = __builtin_convertvector(floatx2{pr[2 * e], pr[2 * e + 1]}, half2_t);
+        ph[2 * e] = h2[0];
+        ph[2 * e + 1] = h2[1];
+      }
+      fence();
+      mm(2);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hf[e] = __builtin_convertvector(half2_t{ph[2 * e], ph[2 * e + 1]}, floatx2);
+      fence();
+      mm(3);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const floatx2 d = floatx2{pr[2 * e], pr[2 * e + 1]} - hf[e];
+        const half2_t l2 = __builtin_convertvector(d, half2_t);
+        pl[2 * e] = l2[0];
+        pl[2 * e + 1] = l2[1];
+      }
+      fence();
+      mm(4);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rs += pr[e];
+      fence();
+      mm(5);
+      lsum += rs;
+      fence();
+      mm(6);
+      fence();
+      mm(7);
+      fence();
+      pv(va, ph, pl);
+      sc[0] = scn[0];
+      sc[1] = scn[1];
+    } else {
+      probs(masked, x, ph, pl);
+      pv(va, ph, pl);
+    }
+  };
+  // The wave's pairs in three runs: those needing the mask (before the window has
+  // passed every column's start), those every column sees whole, and masked ones again
+  // (the causal diagonal and the end of the keys). Pairs outside [pa, pb) only enter
+  // their stages.
+  int wa = pa, wb = pa;
+  if (pa < pb) {
+    const int d = tlo[0] - first_key;
+    wa = d <= 0 ? 0 : (d + 31) / 32;
+    const int e = min(tmin[0] - 31, key_end - 32) - first_key;
+    wb = e < 0 ? 0 : e / 32 + 1;
+    wa = min(max(wa, pa), pb - 1);
+    wb = min(max(wb, wa), pb - 1);
   }
+  stage_enter(0);
+  int i = 0;
+  for (; i < pa; ++i)
+    if ((i & 1) && (i >> 1) + 1 < static_cast<int>(nst)) stage_enter(static_cast<uint32_t>(i >> 1) + 1);
+  if (pa < pb) {
+    qk(pa, sc);
+    for (; i < wa; ++i) step(std::true_type{}, std::true_type{}, i);
+    for (; i < wb; ++i) step(std::false_type{}, std::true_type{}, i);
+    for (; i < pb - 1; ++i) step(std::true_type{}, std::true_type{}, i);
+    step(std::true_type{}, std::false_type{}, i);
+    ++i;
+  }
+  for (; i < npair; ++i)
+    if ((i & 1) && (i >> 1) + 1 < static_cast<int>(nst)) stage_enter(static_cast<uint32_t>(i >> 1) + 1);
   // No load into LDS may land after the workgroup ends.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  const float l = sum_xor32(sum_xor16(lsum));
   const size_t qd = static_cast<size_t>(hq) * kD;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const uint32_t lr = (wave * NT + t) * 16 + c;
     if (lr >= nlog) continue;
     const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
-    float* o = out + rr * qd + h * kD + g * 32;
-    const float inv = 1.0f / l[t];
+    // acc[t][j][i] is dim 16 j + 4 g + i of the column.
+    float* o = out + rr * qd + h * kD + g * 4;
+    const float inv = 1.0f / l;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<float4*>(o + i * 8) =
-          float4{acc[t][0][i] * inv, acc[t][1][i] * inv, acc[t][2][i] * inv, acc[t][3][i] * inv};
-      *reinterpret_cast<float4*>(o + i * 8 + 4) =
-          float4{acc[t][4][i] * inv, acc[t][5][i] * inv, acc[t][6][i] * inv, acc[t][7][i] * inv};
-    }
+    for (int j = 0; j < 8; ++j)
+      *reinterpret_cast<float4*>(o + j * 16) =
+          float4{acc[j][0] * inv, acc[j][1] * inv, acc[j][2] * inv, acc[j][3] * inv};
   }
 }
 
