@@ -50,8 +50,8 @@ static constexpr int kPrefillTiles = 1;  // MFMA tiles (16 logical rows) per wav
 static constexpr int kPrefillRows = kPrefillWaves * kPrefillTiles * 16;  // logical rows per item
 
 static constexpr int kStageBlocks = 4;  // 16-key blocks per LDS stage (64 keys, 32 KiB of K+V)
-static constexpr int kRing = 4;         // LDS stages: kRing - 1 in flight while one is computed
-static constexpr bool kPrefillSplitP = true;  // P as f16 hi + lo (else one f16 rounding)
+static constexpr int kRing = 4;  // LDS stages: kLead in flight, one computed, one finishing
+static constexpr int kLead = kRing - 2;
 static constexpr float kLazyRescale = 8.0f;    // log2 headroom before the maximum moves
 
 // One 16-byte piece per lane from global memory straight into LDS (no registers): lane
@@ -70,19 +70,21 @@ __device__ __forceinline__ void load_to_lds16(const void* src, uint32_t lds) {
       : "memory");
 }
 
-// Two waves per SIMD (at most 256 registers each), so one wave's softmax arithmetic
-// overlaps the other's matrix products.
+// W waves of NT MFMA tiles each (W * NT * 16 = kPrefillRows logical rows); with one wave
+// per SIMD (W = 4) a wave has up to 512 registers and overlaps its own matrix products
+// with its softmax arithmetic (software-pipelined below).
 // QKV: q is not given; the kernel reads its rows' raw q heads from qkv and normalises
 // and rotates them itself, with write_rows' arithmetic (the same bits as
 // qk_norm_rope_append), the key heads having been stored before the launch.
-template <bool QKV>
-__global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_attn_prefill(
+template <bool QKV, int W = kPrefillWaves, int NT = kPrefillTiles>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8 / W))) void paged_attn_prefill(
     const PrefillItem* __restrict__ items, const uint32_t* pos,
     const uint32_t* __restrict__ pages, const _Float16* __restrict__ kc,
     const _Float16* __restrict__ vc, const float* q, float* __restrict__ out,
     uint32_t hq, uint32_t hkv, uint32_t bpp_shift, uint32_t window, float scale_log2,
     QkvIn qi_in) {
-  constexpr int NT = kPrefillTiles, SB = kStageBlocks;
+  constexpr int SB = kStageBlocks;
+  static_assert(W * NT * 16 == kPrefillRows, "a work item's rows are W waves of NT tiles");
   // A ring of stages; each holds SB blocks of K as [p][g][key] (4 KiB each) and then SB
   // blocks of V as [key][128] (4 KiB each).
   __shared__ half8 ring[kRing][2 * SB * 256];
@@ -99,42 +101,54 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
   const uint32_t bpp_mask = (1u << bpp_shift) - 1u;
   const size_t head_stride = static_cast<size_t>(16u << bpp_shift) * kD;
   const uint32_t* pt = pages + it.pt_off;
-  // Each wave moves an eighth of a stage: wave w takes block w / 2 of the stage, its K
-  // (w even) or V (w odd), as four 1 KiB rows. K row p is read transposed ([p][key][g] in
-  // the arena, [p][g][key] in LDS): lane l fetches key l % 16, dims group l / 16. V keeps
-  // its [key][128] rows, but the 32-byte chunks of key k's row are stored XOR-swizzled
-  // (chunk j at j ^ (k & 7)) so that the transposing reads below stay at the minimum of
-  // two passes per 512 bytes; within a 1 KiB row lane l lands on key 4r + l / 16, piece
-  // l % 16, and so fetches the piece that belongs there.
-  static_assert(kPrefillWaves == 8 && SB == 4, "the stage split below assumes 8 waves, 4 blocks");
-  constexpr int kRowsPerWave = 4;  // 1 KiB rows (loads) per wave per stage
-  const uint32_t my_blk = static_cast<uint32_t>(wave >> 1);
-  const bool my_v = (wave & 1) != 0;
-  uint32_t lane_src[kRowsPerWave];
+  // Each wave moves HW of the stage's 2 * SB block halves, half h being block h / 2's K
+  // (h even) or V (h odd), as four 1 KiB rows each. K row p is read transposed ([p][key][g]
+  // in the arena, [p][g][key] in LDS): lane l fetches key l % 16, dims group l / 16. V
+  // keeps its [key][128] rows, but the 32-byte chunks of key k's row are stored
+  // XOR-swizzled (chunk j at j ^ (k & 7)) so that the transposing reads below stay at the
+  // minimum of two passes per 512 bytes; within a 1 KiB row lane l lands on key
+  // 4 r + l / 16, piece l % 16, and so fetches the piece that belongs there.
+  static_assert((2 * SB) % W == 0, "whole block halves per wave");
+  constexpr int HW = 2 * SB / W;
+  constexpr int kRowsPerWave = 4 * HW;  // 1 KiB rows (loads) per wave per stage
+  uint32_t src_k[4], src_v[4];
 #pragma unroll
-  for (int r = 0; r < kRowsPerWave; ++r) {
+  for (int r = 0; r < 4; ++r) {
     const uint32_t key = 4 * r + (lane >> 4), pp = lane & 15;
-    lane_src[r] = my_v ? key * 256u + (2u * ((pp >> 1) ^ (key & 7u)) + (pp & 1u)) * 16u
-                       : static_cast<uint32_t>(r * 1024 + ((lane & 15) * 4 + (lane >> 4)) * 16);
+    src_v[r] = key * 256u + (2u * ((pp >> 1) ^ (key & 7u)) + (pp & 1u)) * 16u;
+    src_k[r] = static_cast<uint32_t>(r * 1024 + ((lane & 15) * 4 + (lane >> 4)) * 16);
   }
-  const char* my_arena = reinterpret_cast<const char*>(my_v ? vc : kc);
   const uint32_t ring_base = static_cast<uint32_t>(
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) half8*)&ring[0][0]));
-  // The page of the block a wave moves for stage st is read one stage ahead, so the
-  // scalar load's latency is not waited for right after the stage's barrier.
-  auto page_of = [&](uint32_t st) {
-    uint32_t b = it.blk0 + st * SB + my_blk;
+  // The pages of the blocks a wave moves for stage st are read one stage ahead, so the
+  // scalar loads' latency is not waited for right after the stage's barrier.
+  auto page_of = [&](uint32_t st, uint32_t blk) __attribute__((always_inline)) {  // (page id, block within the page)
+    uint32_t b = it.blk0 + st * SB + blk;
     b = b < it.blk1 ? b : it.blk1 - 1;  // past the end: re-read the last block (unused)
-    return pt[b >> bpp_shift] * hkv * head_stride + static_cast<size_t>(b & bpp_mask) * 16 * kD;
+    return uint2{pt[b >> bpp_shift], b & bpp_mask};
   };
-  size_t next_elem = page_of(0);
-  auto issue = [&](uint32_t st, uint32_t slot) {  // stage st into ring slot `slot`
-    const char* blk = my_arena + (next_elem + kh * head_stride) * 2;
-    next_elem = page_of(st + 1);
-    const uint32_t dst = ring_base + slot * (2 * SB * 256 * 16) +
-                         (my_v ? SB * 4096u : 0u) + my_blk * 4096u;
+  constexpr int BW = (HW + 1) / 2;  // blocks a wave touches per stage
+  uint2 next_page[BW];
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) load_to_lds16(blk + lane_src[r], dst + r * 1024);
+  for (int bb = 0; bb < BW; ++bb) next_page[bb] = page_of(0, static_cast<uint32_t>((wave * HW) / 2 + bb));
+  auto issue = [&](uint32_t st, uint32_t slot) __attribute__((always_inline)) {  // stage st into ring slot `slot`
+    size_t elem[BW];
+#pragma unroll
+    for (int bb = 0; bb < BW; ++bb) {
+      elem[bb] = (static_cast<size_t>(next_page[bb].x) * hkv + kh) * head_stride +
+                 static_cast<size_t>(next_page[bb].y) * 16 * kD;
+      next_page[bb] = page_of(st + 1, static_cast<uint32_t>((wave * HW) / 2 + bb));
+    }
+#pragma unroll
+    for (int hh = 0; hh < HW; ++hh) {
+      const int h = wave * HW + hh;
+      const uint32_t my_blk = static_cast<uint32_t>(h >> 1);
+      const bool my_v = (h & 1) != 0;
+      const char* blk = reinterpret_cast<const char*>(my_v ? vc : kc) + elem[(hh + (wave * HW) % 2) / 2] * 2;
+      const uint32_t dst = ring_base + slot * (2 * SB * 256 * 16) + (my_v ? SB * 4096u : 0u) + my_blk * 4096u;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) load_to_lds16(blk + (my_v ? src_v[r] : src_k[r]), dst + r * 1024);
+    }
   };
   // q and pos are read first, unconditionally (rows past the tile read row 0 and are
   // zeroed), so that waiting for them does not wait for the K/V stages issued after.
@@ -166,7 +180,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
   __builtin_amdgcn_sched_barrier(0);
   const uint32_t nst = (it.blk1 - it.blk0 + SB - 1) / SB;  // stages
 #pragma unroll
-  for (int j = 0; j < kRing - 1; ++j) issue(j, j);
+  for (int j = 0; j < kLead; ++j) issue(j, j);
 
   if constexpr (QKV) {
     // write_rows for the columns' q heads. Lane g of a column holds dims
@@ -255,12 +269,20 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
     wlo = min(wlo, __builtin_amdgcn_readfirstlane(lo));
   }
 
-  static_assert(NT == 1, "the pipelined loop below takes one MFMA tile per wave");
-  float m = -INFINITY;
-  float lsum = 0.0f;  // this lane's share of its column's sum (its 8 keys of every pair)
-  floatx4 acc[8];
+  // Running maxima start at a finite floor far below any score instead of -inf: a masked
+  // score (-inf) then always gives P = 0, a column that has seen no key yet keeps P = 0,
+  // and its first key rescales (by 2^(floor - s) = 0) the zero state, with no special
+  // cases. Scores are in log2 units of q.k / sqrt(d), far above the floor.
+  constexpr float kFloor = -1.0e30f;
+  float m[NT], lsum[NT];  // lsum: this lane's share of its column's sum (its 8 keys of every pair)
+  floatx4 acc[NT][8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = floatx4{0, 0, 0, 0};
+  for (int t = 0; t < NT; ++t) {
+    m[t] = kFloor;
+    lsum[t] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[t][j] = floatx4{0, 0, 0, 0};
+  }
   const int key_end = static_cast<int>(it.blk1 * 16);
   const int first_key = static_cast<int>(it.blk0 * 16);
   const int npair = static_cast<int>(2 * nst);
@@ -273,6 +295,22 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
     const int e = min(wmax, key_end - 1) - first_key;
     pb = e < 0 ? 0 : min(npair, e / 32 + 1);
   }
+  // Whole pairs (every key visible to every column of the wave, no mask) are [wa, wb).
+  int wtmin = INT32_MAX, wtlo = -1;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    wtmin = min(wtmin, tmin[t]);
+    wtlo = max(wtlo, tlo[t]);
+  }
+  int wa = pa, wb = pa;
+  if (pa < pb) {
+    const int d = wtlo - first_key;
+    wa = d <= 0 ? 0 : (d + 31) / 32;
+    const int e = min(wtmin - 31, key_end - 32) - first_key;
+    wb = e < 0 ? 0 : e / 32 + 1;
+    wa = min(max(wa, pa), pb);
+    wb = min(max(wb, wa), pb);
+  }
 
   // Per lane, the byte offset of its transposing-read address for dim group j within a
   // block of V (see the swizzle above): key k = 4 g + c / 4, dims 16 j + 4 (c % 4).
@@ -284,243 +322,263 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
   }
 
   // Stage st becomes readable: this wave's loads of it are done when at most the
-  // kRing - 2 later stages' are in flight, and the barrier makes every wave's part
-  // visible. Every wave has then also issued and (lgkmcnt) finished its reads of the
-  // stage before st, whose slot is refilled with stage st + kRing - 1.
-  auto stage_enter = [&](uint32_t st) {
-    __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)" ::"n"(kRowsPerWave * (kRing - 2))
+  // kLead - 1 later stages' are in flight, and the barrier makes every wave's part
+  // visible. Every wave has then also issued and (lgkmcnt) finished its reads of stage
+  // st - 2, whose slot is refilled with stage st + kLead (the last pair of stage st - 1
+  // still reads its V after the barrier).
+  auto stage_enter = [&](uint32_t st) __attribute__((always_inline)) {
+    __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)" ::"n"(kRowsPerWave * (kLead - 1))
                      : "memory");
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
-    issue(st + kRing - 1, (st + kRing - 1) & (kRing - 1));
+    issue(st + kLead, (st + kLead) & (kRing - 1));
   };
-  auto pair_lds = [&](int i) {  // LDS byte address of pair i's K (its V is 16 KiB on)
+  // Stage s + 1 is entered halfway through pair 2 s (the first pair of stage s), so that
+  // the second half of that pair can already read pair 2 s + 2's K, one pair ahead.
+  auto enter_mid = [&](int i) __attribute__((always_inline)) {
+    if (!(i & 1) && (i >> 1) + 1 < static_cast<int>(nst)) stage_enter(static_cast<uint32_t>(i >> 1) + 1);
+  };
+  auto pair_lds = [&](int i) __attribute__((always_inline)) {  // LDS byte address of pair i's K (its V is SB * 4 KiB on)
     return ring_base + ((static_cast<uint32_t>(i) >> 1) & (kRing - 1)) * (2 * SB * 256 * 16) +
            (static_cast<uint32_t>(i) & 1u) * 8192u;
   };
-  // S^T of pair i: 2 accumulators (one per block), each taking the hi-part products for
-  // p = 0..3 and then the lo-part ones, 2 MFMAs apart.
-  auto qk = [&](int i, floatx4 (&sc)[2]) {
+  auto read_k1 = [&](int i, half8 (&kk)[2][4], int r) {  // read r (h = r / 4, p = r % 4) of pair i's K
     const half8* kb = reinterpret_cast<const half8*>(
         reinterpret_cast<const char*>(&ring[0][0]) + (pair_lds(i) - ring_base));
-    half8 kk[2][4];
+    kk[r >> 2][r & 3] = kb[(r >> 2) * 256 + (r & 3) * 64 + lane];
+  };
+  auto read_k = [&](int i, half8 (&kk)[2][4]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int p = 0; p < 4; ++p) kk[h][p] = kb[h * 256 + p * 64 + lane];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) sc[h] = floatx4{0, 0, 0, 0};
-#pragma unroll
-    for (int part = 0; part < 2; ++part)
-#pragma unroll
-      for (int p = 0; p < 4; ++p)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk[h][p], part ? ql[0][p] : qh[0][p], sc[h], 0, 0, 0);
+    for (int r = 0; r < 8; ++r) read_k1(i, kk, r);
   };
   // V^T operand of dim group j: row c is dim 16 j + c, element e is key
   // (e / 4) * 16 + 4 g + e % 4 of the pair (the order of P). Each half is one transposing
   // read: in a 16-lane group, lane i receives element i % 4 of the 8 bytes source lane
   // 4 e + i / 4 addressed, so source lane s (= c) addresses key 4 g + s / 4, dims
   // 16 j + 4 (s % 4) .. + 3, at its swizzled place.
-  auto read_v = [&](int i, half8 (&va)[8]) {
+  auto read_v1 = [&](int i, half8 (&va)[8], int j) {  // dim group j of pair i's V
     const uint32_t vb = pair_lds(i) + SB * 4096u;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const lds_half4* p0 = reinterpret_cast<const lds_half4*>(
-          reinterpret_cast<const __attribute__((address_space(3))) char*>(static_cast<uintptr_t>(vb)) + vtr_off[j]);
-      const half4 lo = __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(const_cast<lds_half4*>(p0)));
-      const half4 hi = __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(const_cast<lds_half4*>(p0 + 512)));
-      va[j] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    }
+    const lds_half4* p0 = reinterpret_cast<const lds_half4*>(
+        reinterpret_cast<const __attribute__((address_space(3))) char*>(static_cast<uintptr_t>(vb)) + vtr_off[j]);
+    const half4 lo = __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(const_cast<lds_half4*>(p0)));
+    const half4 hi = __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(const_cast<lds_half4*>(p0 + 512)));
+    va[j] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
-  // Online softmax of pair i for the wave's columns, in two parts. The running maximum
-  // moves only when some column's maximum grew by more than kLazyRescale (or was still
-  // empty): between moves, scores may exceed it by up to that, so P stays below
-  // 2^kLazyRescale, well inside binary16 and f32; the sum uses the same offset, so the
-  // softmax is the same. Part one masks the scores, finds the maxima and, when the
-  // maximum moves (wave-uniform, rare after the first pairs), rescales the accumulators
-  // and the sum in place.
-  auto rescale = [&](auto masked, int i, const floatx4 (&sc)[2], float (&x)[8]) {
-    const int key0 = first_key + 32 * i;
-    float bmax = -INFINITY;
+  auto read_v = [&](int i, half8 (&va)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) read_v1(i, va, j);
+  };
+  // S^T of pair i for tile t: 2 accumulators (one per block); step k of 8 takes dims group
+  // p = k % 4 of q's hi (k < 4) or lo part, so consecutive products into one accumulator
+  // are 2 * NT MFMAs apart.
+  auto qk_mfma = [&](const half8 (&kk)[2][4], floatx4 (&sc)[NT][2], int k, int t) __attribute__((always_inline)) {
+    const int part = k >> 2, p = k & 3;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        if constexpr (decltype(masked)::value) {
-          const int kp = key0 + h * 16 + 4 * g + ii;
-          // Bitwise, not short-circuit: straight-line selects instead of branches.
-          const bool ok = (kp >= rlo[0]) & (kp <= rpos[0]) & (kp < key_end);
-          x[h * 4 + ii] = ok ? sc[h][ii] : -INFINITY;
-        } else {
-          x[h * 4 + ii] = sc[h][ii];
-        }
-        bmax = fmaxf(bmax, x[h * 4 + ii]);
-      }
-    bmax = max_xor32(max_xor16(bmax));
-    const float mn = fmaxf(m, bmax);
-    if (__builtin_amdgcn_ballot_w64(mn > m + kLazyRescale)) {  // wave-uniform
-      // A column still empty after this pair (mn = -inf) keeps its (zero) state.
-      const float corr = mn != -INFINITY ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
-      lsum *= corr;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] *= corr;
-      m = mn;
-    }
+      sc[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk[h][p], part ? ql[t][p] : qh[t][p], sc[t][h], 0, 0, 0);
   };
-  // Part two: P as f16 hi + lo parts (element e of a lane is key (e / 4) * 16 + 4 g + e % 4
-  // of the pair) and this lane's share of the sum. Unmasked pairs are whole for every
-  // column, so m is finite there; a masked column that has seen no key yet (m = -inf)
-  // gets zeros.
-  auto probs = [&](auto masked, const float (&x)[8], half8& ph, half8& pl) {
-    float pr[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if constexpr (decltype(masked)::value)
-        pr[e] = m != -INFINITY ? __builtin_amdgcn_exp2f(x[e] - m) : 0.0f;
-      else
-        pr[e] = __builtin_amdgcn_exp2f(x[e] - m);
-    }
-    float rs = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) rs += pr[e];
-    lsum += rs;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      ph[e] = static_cast<_Float16>(pr[e]);
-      if constexpr (kPrefillSplitP) pl[e] = static_cast<_Float16>(pr[e] - static_cast<float>(ph[e]));
-    }
-  };
-  // O^T += V^T P^T: every dim group's hi product, then every lo product (the two products
-  // into one accumulator 8 MFMAs apart).
-  auto pv = [&](const half8 (&va)[8], const half8& ph, const half8& pl) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[j], ph, acc[j], 0, 0, 0);
-    if constexpr (kPrefillSplitP) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[j], pl, acc[j], 0, 0, 0);
-    }
-  };
-  // One pair step, software-pipelined: this pair's V is read (LDS) while its maxima are
-  // found; the next pair's scores (16 MFMAs) are interleaved with this pair's
-  // exponentials (VALU) in one block; then this pair's products. The scores of pair i
-  // arrive in sc, and pair i + 1's leave in it. At the end of a stage (odd i) the next
-  // stage is entered between this pair's reads and the next pair's.
-  floatx4 sc[2];
-  auto step = [&](auto masked, auto has_next, int i) {
-    half8 va[8];
-    read_v(i, va);
-    float x[8];
-    rescale(masked, i, sc, x);
-    if ((i & 1) && (i >> 1) + 1 < static_cast<int>(nst)) stage_enter(static_cast<uint32_t>(i >> 1) + 1);
-    half8 ph, pl;
-    if constexpr (decltype(has_next)::value) {
-      // The next pair's K, then its 16 score MFMAs two at a time (one per block, so two
-      // independent chains), each couple followed by a slice of this pair's softmax. The
-      // sched_barrier fences keep this order: the matrix pipe runs the products while
-      // the vector pipe does the slices.
-      const half8* kb = reinterpret_cast<const half8*>(
-          reinterpret_cast<const char*>(&ring[0][0]) + (pair_lds(i + 1) - ring_base));
-      half8 kk[2][4];
+  // Maxima of pair i (part one of its online softmax): masked scores, then, when some
+  // column's maximum grew by more than kLazyRescale (wave-uniform, rare after the first
+  // pairs), the accumulators and sums are rescaled in place and the maximum moves.
+  // Between moves, scores may exceed the maximum by up to kLazyRescale, so P stays
+  // below 2^kLazyRescale, well inside binary16 and f32; the sum uses the same offset, so
+  // the softmax is the same.
+  auto maxima_tile = [&](auto masked, int i, const floatx4 (&sc)[NT][2], float (&x)[NT][8], float (&mn)[NT],
+                         int t) __attribute__((always_inline)) {
+    const int key0 = first_key + 32 * i;
+    {
+      float bmax = kFloor;
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int p = 0; p < 4; ++p) kk[h][p] = kb[h * 256 + p * 64 + lane];
-      floatx4 scn[2] = {floatx4{0, 0, 0, 0}, floatx4{0, 0, 0, 0}};
-      float pr[8], rs = 0.0f;
-      floatx2 hf[4];  // ph as f32, pairwise
-      auto mm = [&](int k) {  // score MFMAs k (hi parts p = k, then lo parts p = k - 4)
-        const int p = k & 3;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          scn[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk[h][p], k < 4 ? qh[0][p] : ql[0][p], scn[h], 0, 0, 0);
-      };
-      auto ex = [&](int e) {
-        if constexpr (decltype(masked)::value)
-          pr[e] = m != -INFINITY ? __builtin_amdgcn_exp2f(x[e] - m) : 0.0f;
-        else
-          pr[e] = __builtin_amdgcn_exp2f(x[e] - m);
-      };
-      auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
-      ex(0); ex(1); ex(2); ex(3);
-      fence();
-      mm(0); ex(4); ex(5); ex(6); ex(7);
-      fence();
-      mm(1);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const half2_t h2 = __builtin_convertvector(floatx2{pr[2 * e], pr[2 * e + 1]}, half2_t);
-        ph[2 * e] = h2[0];
-        ph[2 * e + 1] = h2[1];
-      }
-      fence();
-      mm(2);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) hf[e] = __builtin_convertvector(half2_t{ph[2 * e], ph[2 * e + 1]}, floatx2);
-      fence();
-      mm(3);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const floatx2 d = floatx2{pr[2 * e], pr[2 * e + 1]} - hf[e];
-        const half2_t l2 = __builtin_convertvector(d, half2_t);
-        pl[2 * e] = l2[0];
-        pl[2 * e + 1] = l2[1];
-      }
-      fence();
-      mm(4);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) rs += pr[e];
-      fence();
-      mm(5);
-      lsum += rs;
-      fence();
-      mm(6);
-      fence();
-      mm(7);
-      fence();
-      pv(va, ph, pl);
-      sc[0] = scn[0];
-      sc[1] = scn[1];
-    } else {
-      probs(masked, x, ph, pl);
-      pv(va, ph, pl);
+        for (int ii = 0; ii < 4; ++ii) {
+          if constexpr (decltype(masked)::value) {
+            const int kp = key0 + h * 16 + 4 * g + ii;
+            // Bitwise, not short-circuit: straight-line selects instead of branches.
+            const bool ok = (kp >= rlo[t]) & (kp <= rpos[t]) & (kp < key_end);
+            x[t][h * 4 + ii] = ok ? sc[t][h][ii] : -INFINITY;
+          } else {
+            x[t][h * 4 + ii] = sc[t][h][ii];
+          }
+          bmax = fmaxf(bmax, x[t][h * 4 + ii]);
+        }
+      mn[t] = fmaxf(m[t], max_xor32(max_xor16(bmax)));
     }
   };
-  // The wave's pairs in three runs: those needing the mask (before the window has
-  // passed every column's start), those every column sees whole, and masked ones again
-  // (the causal diagonal and the end of the keys). Pairs outside [pa, pb) only enter
-  // their stages.
-  int wa = pa, wb = pa;
-  if (pa < pb) {
-    const int d = tlo[0] - first_key;
-    wa = d <= 0 ? 0 : (d + 31) / 32;
-    const int e = min(tmin[0] - 31, key_end - 32) - first_key;
-    wb = e < 0 ? 0 : e / 32 + 1;
-    wa = min(max(wa, pa), pb - 1);
-    wb = min(max(wb, wa), pb - 1);
-  }
+  auto maxima = [&](auto masked, int i, const floatx4 (&sc)[NT][2], float (&x)[NT][8], float (&mn)[NT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) maxima_tile(masked, i, sc, x, mn, t);
+  };
+  auto rescale = [&](const float (&mn)[NT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (__builtin_amdgcn_ballot_w64(mn[t] > m[t] + kLazyRescale)) {  // wave-uniform
+        const float corr = __builtin_amdgcn_exp2f(m[t] - mn[t]);
+        lsum[t] *= corr;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[t][j] *= corr;
+        m[t] = mn[t];
+      }
+    }
+  };
+  // Part two of pair i's softmax, in 24 slices per tile of 1-3 VALU each: P (element e
+  // of a lane is key (e / 4) * 16 + 4 g + e % 4 of the pair) as f16 hi + lo parts, and
+  // the sum. Slices 0-7 exponentials, 8-11 hi parts, 12-15 hi parts back to f32, 16-19 lo
+  // parts, 20-23 the sum.
+  struct Soft {
+    float pr[NT][8];
+    floatx2 hf[NT][4];
+    half8 ph[NT], pl[NT];
+    float rs[NT];
+  };
+  constexpr int kSlices = 24;
+  auto soft_slice = [&](int k, Soft& sf, const float (&x)[NT][8]) __attribute__((always_inline)) {
+    const int t = k / kSlices, sl = k % kSlices;
+    if (t >= NT) return;
+    if (sl < 8) {
+      sf.pr[t][sl] = __builtin_amdgcn_exp2f(x[t][sl] - m[t]);
+    } else if (sl < 12) {
+      const int e = sl - 8;
+      const half2_t h2 = __builtin_convertvector(floatx2{sf.pr[t][2 * e], sf.pr[t][2 * e + 1]}, half2_t);
+      sf.ph[t][2 * e] = h2[0];
+      sf.ph[t][2 * e + 1] = h2[1];
+    } else if (sl < 16) {
+      const int e = sl - 12;
+      sf.hf[t][e] = __builtin_convertvector(half2_t{sf.ph[t][2 * e], sf.ph[t][2 * e + 1]}, floatx2);
+    } else if (sl < 20) {
+      const int e = sl - 16;
+      const floatx2 d = floatx2{sf.pr[t][2 * e], sf.pr[t][2 * e + 1]} - sf.hf[t][e];
+      const half2_t l2 = __builtin_convertvector(d, half2_t);
+      sf.pl[t][2 * e] = l2[0];
+      sf.pl[t][2 * e + 1] = l2[1];
+    } else {
+      const int e = sl - 20;
+      const float r2 = sf.pr[t][2 * e] + sf.pr[t][2 * e + 1];
+      sf.rs[t] = e == 0 ? r2 : sf.rs[t] + r2;
+      if (e == 3) lsum[t] += sf.rs[t];
+    }
+  };
+  // O^T += V^T P^T for tile t, dim group j (hi product; lo product with lo = true).
+  auto pv_mfma = [&](const half8 (&va)[8], const Soft& sf, int t, int j, bool lo) __attribute__((always_inline)) {
+    acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[j], lo ? sf.pl[t] : sf.ph[t], acc[t][j], 0, 0, 0);
+  };
+  auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
+
+  // One pair step, software-pipelined one pair ahead in both LDS reads and scores. On
+  // entry: pair i + 1's K is in kk, pair i's V in va, pair i's masked scores in x (its
+  // rescale done). Block one: pair i + 1's 16 * NT score MFMAs, each followed by a slice
+  // of pair i's softmax (exponentials, P parts, sums) and, every 16 / (16 NT / 16) MFMAs,
+  // one of pair i + 1's V reads (into vn): the wave issues in order, and an MFMA waiting
+  // for the busy matrix pipe holds back everything behind it, so each one carries some
+  // vector and LDS work. Halfway (even i), the next stage is entered. Block two: pair
+  // i's 16 * NT product MFMAs, interleaved with pair i + 1's maxima and pair i + 2's K
+  // reads (into kk). Then pair i + 1's rescale, if its maximum moved.
+  float x[NT][8];
+  half8 kk[2][4];
+  auto step = [&](auto next_masked, int i, half8 (&va)[8], half8 (&vn)[8]) __attribute__((always_inline)) {
+    floatx4 scn[NT][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) scn[t][0] = scn[t][1] = floatx4{0, 0, 0, 0};
+    Soft sf;
+    constexpr int kMm = 16 * NT;  // score MFMAs
+#pragma unroll
+    for (int q = 0; q < kMm; ++q) {
+      const int k = q / (2 * NT), t = (q / 2) % NT, h = q % 2;
+      const int part = k >> 2, p = k & 3;
+      scn[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk[h][p], part ? ql[t][p] : qh[t][p], scn[t][h], 0, 0, 0);
+#pragma unroll
+      for (int sl = (q * kSlices * NT) / kMm; sl < ((q + 1) * kSlices * NT) / kMm; ++sl) soft_slice(sl, sf, x);
+      if (q % (kMm / 8) == kMm / 8 - 1) read_v1(i + 1, vn, q / (kMm / 8));
+      fence();
+    }
+    enter_mid(i);
+    const bool k_ahead = i + 2 < pb;
+    float mnn[NT];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) pv_mfma(va, sf, t, j, false);
+      if (k_ahead) read_k1(i + 2, kk, j);
+      // The next pair's maxima, tile by tile, between the hi products.
+      if (j % (8 / NT) == 8 / NT - 1) maxima_tile(next_masked, i + 1, scn, x, mnn, j / (8 / NT));
+      fence();
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) pv_mfma(va, sf, t, j, true);
+      fence();
+    }
+    rescale(mnn);
+  };
+  auto last = [&](int i, const half8 (&va)[8]) __attribute__((always_inline)) {
+    Soft sf;
+#pragma unroll
+    for (int k = 0; k < kSlices * NT; ++k) soft_slice(k, sf, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) pv_mfma(va, sf, t, j, false);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) pv_mfma(va, sf, t, j, true);
+    enter_mid(i);
+  };
+
   stage_enter(0);
   int i = 0;
-  for (; i < pa; ++i)
-    if ((i & 1) && (i >> 1) + 1 < static_cast<int>(nst)) stage_enter(static_cast<uint32_t>(i >> 1) + 1);
+  for (; i < pa; ++i) enter_mid(i);
   if (pa < pb) {
-    qk(pa, sc);
-    for (; i < wa; ++i) step(std::true_type{}, std::true_type{}, i);
-    for (; i < wb; ++i) step(std::false_type{}, std::true_type{}, i);
-    for (; i < pb - 1; ++i) step(std::true_type{}, std::true_type{}, i);
-    step(std::true_type{}, std::false_type{}, i);
+    half8 vaA[8], vaB[8];
+    {  // The first pair's scores, maxima and V, and the next pair's K.
+      read_k(pa, kk);
+      floatx4 sc[NT][2];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) sc[t][0] = sc[t][1] = floatx4{0, 0, 0, 0};
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) qk_mfma(kk, sc, k, t);
+      read_v(pa, vaA);
+      if (pa + 1 < pb) read_k(pa + 1, kk);
+      float mn[NT];
+      if (pa >= wa && pa < wb)
+        maxima(std::false_type{}, pa, sc, x, mn);
+      else
+        maxima(std::true_type{}, pa, sc, x, mn);
+      rescale(mn);
+    }
+    // Steps by the kind of their next pair: masked before wa, whole in [wa, wb), masked
+    // from wb. Two steps per turn, so that the V registers swap roles without copies.
+    auto run = [&](auto next_masked, int i0, int end) __attribute__((always_inline)) {
+      int ii = i0;
+      for (; ii + 2 < end; ii += 2) {
+        step(next_masked, ii, vaA, vaB);
+        step(next_masked, ii + 1, vaB, vaA);
+      }
+      if (ii + 1 < end) {
+        step(next_masked, ii, vaA, vaB);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vaA[j] = vaB[j];
+        ++ii;
+      }
+      return ii;
+    };
+    i = run(std::true_type{}, i, min(wa, pb));
+    i = run(std::false_type{}, i, wb);
+    i = run(std::true_type{}, i, pb);
+    last(i, vaA);
     ++i;
   }
-  for (; i < npair; ++i)
-    if ((i & 1) && (i >> 1) + 1 < static_cast<int>(nst)) stage_enter(static_cast<uint32_t>(i >> 1) + 1);
+  for (; i < npair; ++i) enter_mid(i);
   // No load into LDS may land after the workgroup ends.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  const float l = sum_xor32(sum_xor16(lsum));
   const size_t qd = static_cast<size_t>(hq) * kD;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
+    const float l = sum_xor32(sum_xor16(lsum[t]));
     const uint32_t lr = (wave * NT + t) * 16 + c;
     if (lr >= nlog) continue;
     const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
@@ -530,7 +588,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       *reinterpret_cast<float4*>(o + j * 16) =
-          float4{acc[j][0] * inv, acc[j][1] * inv, acc[j][2] * inv, acc[j][3] * inv};
+          float4{acc[t][j][0] * inv, acc[t][j][1] * inv, acc[t][j][2] * inv, acc[t][j][3] * inv};
   }
 }
 
