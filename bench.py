@@ -401,6 +401,22 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
                                         "GBs": round(nbytes / us / 1e3, 1),
                                         "kv_bytes_per_layer": nbytes}
         kv.destroy()
+        # cfg3's chunked prefill on an f32 arena: the f32 prefill kernel (exact f32
+        # MFMA products), and the same pass through the f32 split-K decode kernel.
+        cache, pr, pool, prior = cfg3_pass(KvCache)
+        kv = hip.new_kv(layers, pool, PAGE, HKV, D, f32=True)
+        _fill_arena(hip, kv, layers, SEED + 3)
+        n = max(2, steps // 2)
+        k_us = _time_attention_kernel(hip, kv, pr, layers, HQ, n)
+        hip.set_option("prefill_min_rows", 1 << 20)
+        k_split = _time_attention_kernel(hip, kv, pr, layers, HQ, n)
+        hip.set_option("prefill_min_rows", 32)
+        flops = sum(4 * HQ * D * (256 * p + 256 * 257 // 2) for p in prior)
+        res["cfg3_chunked_prefill_f32"] = {"attn_kernel_us": round(k_us, 2),
+                                           "TFLOPs": round(flops / k_us / 1e6, 2),
+                                           "f32_mfma_util_vs_157.3TF": round(flops / k_us / 1e6 / 157.3, 4),
+                                           "split_k_decode_kernel_us": round(k_split, 2)}
+        kv.destroy()
     if want('step'):
         # The step after attention at the headline's decode shape: o_proj (16 rows of
         # hq * 128 = 2048 against a bf16 [2048][2048] weight) and the greedy pick over a

@@ -15,6 +15,7 @@
 #include "../../include/yaxus_hip.h"
 #include "attn_decode.hpp"
 #include "attn_prefill.hpp"
+#include "attn_prefill_f32.hpp"
 #include "kv_kernels.hpp"
 #include "qk_rope.hpp"
 #include "step_after.hpp"
@@ -403,8 +404,8 @@ int check_kv(yx_ctx* c, yx_kv* kv, size_t layer) {
 // Builds the split-K work list of the current pass for (window, hq, hkv).
 static constexpr uint32_t kFanIn = 32;  // chunks per group the automatic split aims at most
 
-// f32: the plan of the f32-arena kernel (split-K decode for every pass, 16 logical rows
-// per work item).
+// f32: the f32 arena's plan: its prefill kernel's items for passes with many rows per
+// sequence (as for f16), else its split-K decode kernel's (16 logical rows per item).
 // page_size: the arena's (shared prefixes are found by page ids).
 int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t page_size,
                AttnPlan** out) {
@@ -417,10 +418,12 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
   const size_t G = hq / hkv;
   uint32_t max_rows = 0;
   for (const Group& g : c->groups) max_rows = std::max(max_rows, g.n);
-  if (!f32 && max_rows >= static_cast<uint32_t>(c->prefill_min_rows)) {
-    // Tiles of kPrefillRows logical rows: consecutive rows of one sequence.
+  if (max_rows >= static_cast<uint32_t>(c->prefill_min_rows)) {
+    // Tiles of kPrefillRows logical rows: consecutive rows of one sequence (the f16 and
+    // the f32 arena's prefill kernels take the same items).
     AttnPlan plan;
     plan.prefill = true;
+    plan.f32 = f32;
     const uint32_t per = static_cast<uint32_t>(std::max<size_t>(1, yx::kPrefillRows / G));
     if (G > static_cast<size_t>(yx::kPrefillRows))
       return fail(YX_ERR_UNSUPPORTED, "more query heads per KV head than a prefill tile holds");
@@ -821,8 +824,8 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     if ((rc = append_impl(c, kv, layer, knew, vnew))) return rc;
     knew = vnew = nullptr;
   }
-  if (qkv && plan->prefill) {
-    // The prefill kernel normalises and rotates its rows' q heads itself; K/V first.
+  if (qkv && plan->prefill && !plan->f32) {
+    // The f16 prefill kernel normalises and rotates its rows' q heads itself; K/V first.
     if ((rc = qk_rope_impl(c, kv, layer, *qkv, hq, nullptr, true))) return rc;
   } else if (qkv && (plan->f32 || !(plan->fusable && (plan->wide ? plan->nt <= 2 : plan->balanced)))) {
     // (Two-tile passes keep write_rows as its own launch: fused, each work item
@@ -839,7 +842,15 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     hipEvent_t e0;
     if ((rc = prof_begin(c, YX_KERNEL_ATTENTION, &e0))) return rc;
     const dim3 pgrid(static_cast<unsigned>(plan->pitems.size() * hkv));
-    if (qkv)
+    if (plan->f32)
+      hipLaunchKernelGGL(yx::paged_attn_prefill_f32, pgrid, dim3(64 * yx::kPf32Waves), 0, c->stream,
+                         static_cast<const yx::PrefillItem*>(d_items), c->dev_pos,
+                         static_cast<const uint32_t*>(c->d_pages.p),
+                         reinterpret_cast<const float*>(kv->k[layer]),
+                         reinterpret_cast<const float*>(kv->v[layer]), q, out,
+                         static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv), shift,
+                         static_cast<uint32_t>(window), scale * yx::kLog2e);
+    else if (qkv)
       hipLaunchKernelGGL((yx::paged_attn_prefill<true>), pgrid, dim3(64 * yx::kPrefillWaves), 0, c->stream,
                        static_cast<const yx::PrefillItem*>(d_items),
                        c->dev_pos, static_cast<const uint32_t*>(c->d_pages.p),
