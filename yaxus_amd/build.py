@@ -49,11 +49,17 @@ def build_hip():
 NATIVE_LOOP = os.path.join(ROOT, "tests", "native", "decode_loop")
 
 
+NATIVE_FORK = os.path.join(ROOT, "tests", "native", "fork_rollback")
+
+
 def build_native_tests():
-    """The C++ decode loop over the C ABIs (tests/native), linked to the libraries above."""
+    """The C++ programs over the C ABIs (tests/native), linked to the libraries above: the
+    decode loop, and cfg5's fork and rollback (allocator only)."""
     _run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", NATIVE_LOOP + ".cpp",
           "-L" + HERE, "-lyaxus_hip", "-lyaxus_kv", "-Wl,-rpath,$ORIGIN/../../yaxus_amd",
           "-o", NATIVE_LOOP])
+    _run(["g++", "-O2", "-std=c++17", "-Wall", "-Wextra", NATIVE_FORK + ".cpp",
+          "-L" + HERE, "-lyaxus_kv", "-Wl,-rpath,$ORIGIN/../../yaxus_amd", "-o", NATIVE_FORK])
 
 
 def build_oracle():
