@@ -3,12 +3,15 @@
 // The same arithmetic as `LayerPass::attend` (crates/yaxus-backend-cpu/src/lib.rs:
 // 389-427) for passes with many rows per sequence, the shape the reference's tiled
 // kernel serves (ATTN_TILE, crates/yaxus-backend-gpu/src/shaders.rs:422-592: 32 rows x
-// 32-key blocks, f32 SIMT). Here a workgroup of 8 waves (two per SIMD) takes a tile of
-// kPrefillRows logical rows, the (row, query head) pairs of consecutive rows of one
+// 32-key blocks, f32 SIMT). Here a workgroup of 4 waves (one per SIMD) takes a tile of
+// kPrefillRows = 64 logical rows, the (row, query head) pairs of consecutive rows of one
 // sequence and one KV head; each wave owns 16 of them, the 16 columns of its MFMA tile.
-// Keys stream from HBM straight into a 4-stage LDS ring of 64-key stages
-// (global_load_lds_dwordx4, no registers; three stages in flight while one is computed),
-// and every wave reads them there. Per 32 keys:
+// Keys stream from HBM straight into a 4-slot LDS ring of 32-key stages (64 KiB;
+// global_load_lds_dwordx4, no registers; two stages in flight), and every wave reads
+// them there. Two workgroups share a CU (two waves per SIMD, at most 256 registers each)
+// and run out of phase, so one's start, barriers and output overlap the other's
+// products (cfg3: 86-87 us against 90-91 with one 8-wave workgroup of 128 rows and a
+// 128 KiB ring of 64-key stages per CU). Per 32 keys:
 //   S^T[key][row] = K . Q^T      8 x v_mfma_f32_16x16x32_f16 per tile (q as hi + lo f16)
 //   online softmax per column, once per 32 keys (permlane swaps across lane groups);
 //   the accumulator is rescaled only when a column's maximum grew by more than
@@ -45,11 +48,11 @@ struct PrefillItem {
   uint32_t pad[3];
 };
 
-static constexpr int kPrefillWaves = 8;
+static constexpr int kPrefillWaves = 4;
 static constexpr int kPrefillTiles = 1;  // MFMA tiles (16 logical rows) per wave
 static constexpr int kPrefillRows = kPrefillWaves * kPrefillTiles * 16;  // logical rows per item
 
-static constexpr int kStageBlocks = 4;  // 16-key blocks per LDS stage (64 keys, 32 KiB of K+V)
+static constexpr int kStageBlocks = 2;  // 16-key blocks per LDS stage (32 keys, 16 KiB of K+V)
 static constexpr int kRing = 4;  // LDS stages: kLead in flight, one computed, one finishing
 static constexpr int kLead = kRing - 2;
 static constexpr float kLazyRescale = 8.0f;    // log2 headroom before the maximum moves
@@ -70,20 +73,23 @@ __device__ __forceinline__ void load_to_lds16(const void* src, uint32_t lds) {
       : "memory");
 }
 
-// W waves of NT MFMA tiles each (W * NT * 16 = kPrefillRows logical rows); with one wave
-// per SIMD (W = 4) a wave has up to 512 registers and overlaps its own matrix products
-// with its softmax arithmetic (software-pipelined below).
+// W waves of NT MFMA tiles each (W * NT * 16 = kPrefillRows logical rows) over stages of
+// SBT blocks; 8 / W waves per SIMD (an 8-wave workgroup fills a CU; two 4-wave ones share
+// it). Each wave overlaps its own matrix products with its softmax arithmetic
+// (software-pipelined below).
 // QKV: q is not given; the kernel reads its rows' raw q heads from qkv and normalises
 // and rotates them itself, with write_rows' arithmetic (the same bits as
 // qk_norm_rope_append), the key heads having been stored before the launch.
-template <bool QKV, int W = kPrefillWaves, int NT = kPrefillTiles>
+template <bool QKV, int W = kPrefillWaves, int NT = kPrefillTiles, int SBT = kStageBlocks>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8 / W))) void paged_attn_prefill(
     const PrefillItem* __restrict__ items, const uint32_t* pos,
     const uint32_t* __restrict__ pages, const _Float16* __restrict__ kc,
     const _Float16* __restrict__ vc, const float* q, float* __restrict__ out,
     uint32_t hq, uint32_t hkv, uint32_t bpp_shift, uint32_t window, float scale_log2,
     QkvIn qi_in) {
-  constexpr int SB = kStageBlocks;
+  constexpr int SB = SBT;
+  static_assert(SB == 2 || SB == 4, "stages of one or two pairs of blocks");
+  constexpr int PPS = SB / 2;  // pairs of 16-key blocks per stage
   static_assert(W * NT * 16 == kPrefillRows, "a work item's rows are W waves of NT tiles");
   // A ring of stages; each holds SB blocks of K as [p][g][key] (4 KiB each) and then SB
   // blocks of V as [key][128] (4 KiB each).
@@ -285,7 +291,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   }
   const int key_end = static_cast<int>(it.blk1 * 16);
   const int first_key = static_cast<int>(it.blk0 * 16);
-  const int npair = static_cast<int>(2 * nst);
+  const int npair = static_cast<int>(PPS * nst);
   // Pair i holds keys first_key + 32 i .. + 31. This wave computes the pairs [pa, pb) that
   // hold a key some column of the wave can see; the others it only passes through.
   int pa = npair, pb = npair;
@@ -333,14 +339,18 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
     __asm__ volatile("" ::: "memory");
     issue(st + kLead, (st + kLead) & (kRing - 1));
   };
-  // Stage s + 1 is entered halfway through pair 2 s (the first pair of stage s), so that
-  // the second half of that pair can already read pair 2 s + 2's K, one pair ahead.
+  // The stage holding pair i + 2 is entered halfway through pair i (when pair i + 2 is
+  // the first pair of its stage), so that the second half of pair i can already read
+  // pair i + 2's K. Its slot's previous stage was last read in the first half of the
+  // pair after that stage's last pair, which every wave has passed: kLead <= kRing - 2.
+  static_assert(kLead <= kRing - 2, "a refilled slot is no longer read");
   auto enter_mid = [&](int i) __attribute__((always_inline)) {
-    if (!(i & 1) && (i >> 1) + 1 < static_cast<int>(nst)) stage_enter(static_cast<uint32_t>(i >> 1) + 1);
+    const int j = i + 2;
+    if (j % PPS == 0 && j / PPS < static_cast<int>(nst)) stage_enter(static_cast<uint32_t>(j / PPS));
   };
   auto pair_lds = [&](int i) __attribute__((always_inline)) {  // LDS byte address of pair i's K (its V is SB * 4 KiB on)
-    return ring_base + ((static_cast<uint32_t>(i) >> 1) & (kRing - 1)) * (2 * SB * 256 * 16) +
-           (static_cast<uint32_t>(i) & 1u) * 8192u;
+    return ring_base + ((static_cast<uint32_t>(i) / PPS) & (kRing - 1)) * (2 * SB * 256 * 16) +
+           (static_cast<uint32_t>(i) % PPS) * 8192u;
   };
   auto read_k1 = [&](int i, half8 (&kk)[2][4], int r) {  // read r (h = r / 4, p = r % 4) of pair i's K
     const half8* kb = reinterpret_cast<const half8*>(
@@ -526,7 +536,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
     enter_mid(i);
   };
 
-  stage_enter(0);
+  stage_enter(0);  // pairs 0 .. PPS - 1
+  if (PPS == 1 && nst > 1) stage_enter(1);
   int i = 0;
   for (; i < pa; ++i) enter_mid(i);
   if (pa < pb) {

@@ -5,9 +5,9 @@
 // accumulation, so no operand is rounded to a narrower type and every finite f32 K/V
 // value the reference accepts is served.
 //
-// Work items are the f16 prefill kernel's: kPrefillRows logical rows (consecutive rows of
-// one sequence, all query heads of one KV head) per workgroup of 8 waves, 16 columns per
-// wave. Keys stream from HBM into a 4-slot LDS ring of 32-key stages (two blocks of 16;
+// Work items are built as for the f16 prefill kernel, with kPf32Rows = 128 logical rows
+// (consecutive rows of one sequence, all query heads of one KV head) per workgroup of 8
+// waves, 16 columns per wave. Keys stream from HBM into a 4-slot LDS ring of 32-key stages (two blocks of 16;
 // global_load_lds_dwordx4, three stages in flight while one is computed), laid out in
 // operand order so that every LDS read is one contiguous 1 KiB per wave. Per block of 16
 // keys and wave:
@@ -30,9 +30,9 @@
 namespace yx {
 
 static constexpr int kPf32Waves = 8;
+static constexpr int kPf32Rows = kPf32Waves * 16;  // logical rows per work item (one tile per wave)
 static constexpr int kPf32Ring = 4;               // LDS stages (32 KiB each)
 static constexpr int kPf32Lead = kPf32Ring - 1;   // stages in flight ahead of the one computed
-static_assert(kPf32Waves * 16 == kPrefillRows, "one 16-column tile per wave");
 
 __global__ __launch_bounds__(64 * kPf32Waves) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_attn_prefill_f32(
     const PrefillItem* __restrict__ items, const uint32_t* pos,

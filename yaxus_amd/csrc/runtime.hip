@@ -424,8 +424,9 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
     AttnPlan plan;
     plan.prefill = true;
     plan.f32 = f32;
-    const uint32_t per = static_cast<uint32_t>(std::max<size_t>(1, yx::kPrefillRows / G));
-    if (G > static_cast<size_t>(yx::kPrefillRows))
+    const size_t tile_rows = f32 ? yx::kPf32Rows : yx::kPrefillRows;
+    const uint32_t per = static_cast<uint32_t>(std::max<size_t>(1, tile_rows / G));
+    if (G > tile_rows)
       return fail(YX_ERR_UNSUPPORTED, "more query heads per KV head than a prefill tile holds");
     for (const Group& g : c->groups)
       for (uint32_t r = 0; r < g.n; r += per) {
