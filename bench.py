@@ -388,6 +388,14 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
                                    "verify_logical_GBs": round(bytes_verify / us_verify / 1e3, 1),
                                    "fork_copies": len(copies), "copy_us_all_layers": round(copy_us, 2),
                                    "host_fork_rollback_us": round(host_us, 1)}
+        # The same host work through the allocator's C ABI from C++ (no Python per call).
+        exe = os.path.join(ROOT, "tests", "native", "fork_rollback")
+        if os.path.exists(exe):
+            import subprocess
+            r = subprocess.run([exe, "50"], capture_output=True, text=True, timeout=60)
+            if r.returncode == 0:
+                nat = json.loads(r.stdout.strip().splitlines()[-1])
+                res["cfg5_verify_fork"]["host_fork_rollback_us_native"] = nat["host_fork_rollback_us_median"]
         kv.destroy()
     if want('f32'):
         # The headline's pass on an f32 arena (the reference's K/V precision): twice
