@@ -348,8 +348,11 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
         flops = sum(4 * HQ * D * (256 * p + 256 * 257 // 2) for p in prior)
         wr_us, wr_bytes = _time_write_rows(hip, kv, pr, layers, max(2, steps // 2))
         k_us = _time_attention_kernel(hip, kv, pr, layers, HQ, max(2, steps // 2))
+        ba_one, ba_two = _time_backend_attention(hip, kv, pr, layers, max(2, steps // 2))
         # us_per_layer_step: the K/V append launch plus the prefill kernel, graph-replayed;
-        # attn_kernel_us: the prefill kernel alone (HIP events around each launch).
+        # attn_kernel_us: the prefill kernel alone (HIP events around each launch);
+        # backend_attention_us: Backend::attention from qkv (write_rows' K/V part, then
+        # the prefill kernel normalising and rotating its q heads itself).
         res["cfg3_chunked_prefill"] = {"us_per_layer_step": round(us, 2),
                                        "TFLOPs": round(flops / us / 1e6, 2),
                                        "mfma_util_vs_2.5PF": round(flops / us / 1e6 / 2500.0, 4),
@@ -358,7 +361,9 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
                                        "attn_kernel_mfma_util_vs_2.5PF": round(flops / k_us / 1e6 / 2500.0, 4),
                                        "flops_per_layer": flops,
                                        "write_rows_us_per_layer": round(wr_us, 2),
-                                       "write_rows_GBs": round(wr_bytes / wr_us / 1e3, 1)}
+                                       "write_rows_GBs": round(wr_bytes / wr_us / 1e3, 1),
+                                       "backend_attention_us": round(ba_one, 2),
+                                       "write_rows_then_attention_us": round(ba_two, 2)}
         kv.destroy()
     if want('cfg5'):
         # cfg5: the verify pass over 24 layers; then 8 requests fork from a partly
