@@ -29,11 +29,15 @@ int fail(int code, const std::string& m) {
   return code;
 }
 
+// A failed call's error is also taken out of HIP's per-thread last error, so that a
+// refused allocation is not reported again by the next launch's hipGetLastError().
 #define YX_HIP(call)                                                                    \
   do {                                                                                  \
     hipError_t e_ = (call);                                                             \
-    if (e_ != hipSuccess)                                                               \
+    if (e_ != hipSuccess) {                                                             \
+      (void)hipGetLastError();                                                          \
       return fail(YX_ERR_HIP, std::string(#call) + ": " + hipGetErrorString(e_));       \
+    }                                                                                   \
   } while (0)
 
 // A device buffer that only grows. Growing waits for the stream (the old buffer may
@@ -1125,6 +1129,7 @@ int yx_kv_create(yx_ctx* c, size_t layers, size_t pages, size_t page_size, size_
     if (e == hipSuccess) e = hipMemsetAsync(kp, 0, bytes, c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(vp, 0, bytes, c->stream);
     if (e != hipSuccess) {
+      (void)hipGetLastError();  // as in YX_HIP
       if (kp) (void)hipFree(kp);
       if (vp) (void)hipFree(vp);
       yx_kv_destroy(c, kv);
