@@ -7,7 +7,7 @@ import pytest
 
 from oracle.attn import OracleArena, normal
 from tests.scenario import close
-from yaxus_amd.engine import Engine, EngineConfig, Request
+from yaxus_amd.engine import Engine, EngineConfig, Finish, Request
 from yaxus_amd.model import PagedModel
 
 pytestmark = pytest.mark.gpu
@@ -118,3 +118,40 @@ def test_speculative_matches_plain(hip):
     assert set(plain) == set(spec)
     for key in plain:
         assert close(spec[key], plain[key]).all(), key
+
+
+def test_cancelling_everything_leaves_a_clean_engine(hip):
+    """Reference vs_cpu.rs:209-255 `cancelling_everything_leaves_a_clean_engine`, at the
+    attention level: with two requests running and one waiting, cancelling all three
+    ends each as cancelled, leaves no stream, no waiting request and every KV page
+    free, and the engine then answers a request as it did before."""
+    model = PagedModel(hip, PAGES, max_pos=4096, page=PAGE, layers=LAYERS, hkv=HKV, hq=HQ,
+                       windows=[0, 64], chunk=96)
+    model.set_prefix_cache(False)
+    eng = Recording(model, EngineConfig(max_streams=2, decode_rows=4, busy_prefill_rows=32),
+                    token_fn=token_fn)
+    prompt = [(t * 11) % 90 + 1 for t in range(100)]
+
+    def answer(rid):
+        eng.record = {}
+        eng.submit(Request(rid, prompt, 16))
+        assert eng.run_all() == [(rid, Finish.LENGTH)]
+        return {(p, layer): o for (r, p, layer), o in eng.record.items() if r == rid}
+
+    before = answer(100)
+    free = model.free_pages()
+    for i in range(3):
+        eng.submit(Request(i, prompt, 64))
+    for _ in range(3):
+        eng.step()
+    assert eng.active() > 0 and len(eng.waiting) > 0
+    for i in range(3):
+        assert eng.cancel(i)
+    ended = sorted(eng.run_all(), key=lambda e: e[0])
+    assert ended == [(0, Finish.CANCELLED), (1, Finish.CANCELLED), (2, Finish.CANCELLED)]
+    assert eng.is_idle()
+    assert model.free_pages() == free
+    after = answer(101)
+    assert set(after) == set(before)
+    for key in before:
+        assert np.array_equal(after[key], before[key]), key  # deterministic kernels
