@@ -64,3 +64,52 @@ def test_argmax_rows_matches_the_cpu_backend(hip):
             got.free()
         finally:
             d.free()
+
+
+def test_matmul_rows_do_not_depend_on_the_pass(hip):
+    """Reference crates/yaxus-backend-gpu/tests/kernels.rs:250-321 (rows alone, and as rows
+    of passes of 3 and 7, against the 16-row pass): a row's output has the same bits
+    whatever other rows share its pass, for passes of up to 16 rows (one row tile: the
+    split of k over workgroups depends only on the tile count), so batching decode rows
+    cannot change a sequence's logits."""
+    k, n = 1536, 200
+    x = normal(16 * k, 31, 5).reshape(16, k)
+    w = _bf16_bits(normal(n * k, 32, 6).reshape(n, k))
+    dw = hip.tensor(w.shape, np.uint16).upload(w)
+
+    def run(rows):
+        dx = hip.tensor(rows.shape).upload(np.ascontiguousarray(rows))
+        try:
+            return hip.matmul_bf16(dx, dw).numpy()
+        finally:
+            dx.free()
+
+    try:
+        full = run(x)
+        for start, t in [(0, 1), (5, 1), (15, 1), (2, 3), (8, 7)]:
+            part = run(x[start:start + t])
+            assert np.array_equal(part.view(np.uint32), full[start:start + t].view(np.uint32)), (start, t)
+    finally:
+        dw.free()
+
+
+@pytest.mark.parametrize("rows", [1, 64, 65, 300, 512, 1100])
+def test_argmax_handles_a_whole_pass(hip, rows):
+    """Reference kernels.rs:322-343: a planted maximum per row over passes of up to 1100
+    rows; a row of only -inf or only NaN gives index 0."""
+    cols = 1000
+    x = np.clip(normal(rows * cols, rows, 0), -4.0, 4.0).reshape(rows, cols)  # below the planted 5
+    want = np.array([(r * 37) % cols for r in range(rows)], np.uint32)
+    x[np.arange(rows), want] = 5.0
+    if rows >= 2:
+        x[0, :] = -np.inf
+        x[1, :] = np.nan
+        want[0] = want[1] = 0
+    d = hip.tensor(x.shape).upload(x)
+    try:
+        got = hip.argmax_rows(d)
+        np.testing.assert_array_equal(got.numpy(), want)
+        np.testing.assert_array_equal(got.numpy(), argmax_rows(x))
+        got.free()
+    finally:
+        d.free()
