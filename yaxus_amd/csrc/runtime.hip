@@ -10,6 +10,7 @@
 #include <mutex>
 #include <string>
 #include <tuple>
+#include <unordered_set>
 #include <vector>
 
 #include "../../include/yaxus_hip.h"
@@ -1287,13 +1288,15 @@ int yx_pass_begin(yx_ctx* c, size_t rows, const uint32_t* pos, const uint32_t* k
   if (rows && (!pos || !kv_slot || !pt_off)) return fail(YX_ERR_INVALID, "null row metadata");
   if (npages && !pages) return fail(YX_ERR_INVALID, "null page tables");
   if (rows > 0x7fffffff || npages > 0x7fffffff) return fail(YX_ERR_INVALID, "pass too large");
-  // Every key a row can see must have a page-table entry.
-  for (size_t i = 0; i < rows; ++i) {
-    if (static_cast<uint64_t>(pt_off[i]) >= npages)
-      return fail(YX_ERR_INVALID, "row page table offset beyond the page tables");
-    if (i > 0 && pt_off[i] != pt_off[i - 1]) {
-      for (size_t j = 0; j < i; ++j)
-        if (pt_off[j] == pt_off[i]) return fail(YX_ERR_INVALID, "rows of one sequence are not consecutive");
+  // Every key a row can see must have a page-table entry; a sequence's rows (one page
+  // table) are consecutive.
+  {
+    std::unordered_set<uint32_t> seen;
+    for (size_t i = 0; i < rows; ++i) {
+      if (static_cast<uint64_t>(pt_off[i]) >= npages)
+        return fail(YX_ERR_INVALID, "row page table offset beyond the page tables");
+      if ((i == 0 || pt_off[i] != pt_off[i - 1]) && !seen.insert(pt_off[i]).second)
+        return fail(YX_ERR_INVALID, "rows of one sequence are not consecutive");
     }
   }
   int rc = c->set_device();
