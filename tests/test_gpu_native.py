@@ -20,5 +20,7 @@ def test_native_decode_loop_runs():
     assert r.returncode == 0, r.stderr
     d = json.loads(r.stdout.strip().splitlines()[-1])
     print(d)
-    assert 0 < d["attention_us_all_layers"] <= d["step_us_median"]
+    # One timed run of the launches against the median step that contains them: a 5%
+    # allowance for the single sample's spread.
+    assert 0 < d["attention_us_all_layers"] <= 1.05 * d["step_us_median"]
     assert 0 < d["host_us_median"] < d["step_us_median"]
