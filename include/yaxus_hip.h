@@ -64,12 +64,16 @@ int yx_sync(yx_ctx* ctx);
  * every decode pass). "attn_cascade" (1, the default: consecutive groups of a one-tile
  * decode pass whose page tables start with the same pages, e.g. forks of one prompt,
  * attend those shared keys once for all their rows and merge that result into each
- * row's own; 0: every group reads its whole context). Setting an option drops
- * cached work lists. Values are positive; 0 is accepted for attn_target_waves,
- * attn_decode_shape and attn_cascade. */
+ * row's own; 0: every group reads its whole context). "prefill_split" (1, the default:
+ * prefill tiles much longer than the average load of a workgroup slot, e.g. a chunk of
+ * one long sequence, are split along keys and their partial results merged; 0: every
+ * tile is one work item). Setting an option drops cached work lists. Values are
+ * positive; 0 is accepted for attn_target_waves, attn_decode_shape, attn_cascade and
+ * prefill_split. */
 int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
 /* Counters of the context since its creation: "page_entries_sent" (page-table entries
- * yx_pass_begin uploaded) and "page_runs_sent" (runs of consecutive entries they formed).
+ * yx_pass_begin uploaded), "page_runs_sent" (runs of consecutive entries they formed)
+ * and "prefill_split_tiles" (prefill tiles split along keys in the work lists built).
  * A pass whose groups keep their order and fit the device regions of the previous pass
  * sends only the entries that changed. */
 int yx_ctx_get_stat(yx_ctx* ctx, const char* key, uint64_t* out);

@@ -257,6 +257,43 @@ def test_prefill_tiles_match_oracle(hip, hq, hkv, page, window, chunk):
     assert err < 2e-5, f"max abs err {err}"
 
 
+@pytest.mark.parametrize("hq,hkv,page,window,prior,chunk,f32", [
+    (16, 4, 16, 0, 3000, 64, False), (16, 4, 16, 2000, 3000, 64, False),
+    (8, 2, 32, 0, 5000, 33, False), (32, 2, 16, 0, 2500, 40, False),
+    (16, 4, 64, 0, 4100, 256, False), (16, 4, 16, 0, 4000, 64, True),
+    (8, 2, 32, 1500, 5000, 130, True)])
+def test_prefill_split_along_keys(hip, hq, hkv, page, window, prior, chunk, f32):
+    """One long sequence's chunk: too few tiles to fill the GPU, so each tile's keys are
+    split over several work items whose partial softmaxes the tile's last chunk merges.
+    Against the oracle (to 2e-5), against the same pass with the split off, and bit for
+    bit from call to call (the merge runs in chunk order). A second, short sequence in
+    the same pass keeps its tiles whole. Both arenas (binary16, and f32 with its own
+    prefill kernel)."""
+    sc = Scenario(hip, pages=(prior + chunk) // page + 64, page=page, hkv=hkv, pool_seed=7, f32=f32)
+    a, b = sc.cache.new_seq(), sc.cache.new_seq()
+    sc.prefill({a: prior, b: 40})
+    pr = sc.run_pass([(a, chunk), (b, 20)])
+    sc.store(pr)
+    rows = len(pr.meta.pos)
+    q = sc.draw(rows * hq * D).reshape(rows, hq * D)
+    want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
+    split0 = hip.stat("prefill_split_tiles")
+    got = hip.attend(sc.kv, 0, q, hq, window=window)
+    assert hip.stat("prefill_split_tiles") > split0  # the long sequence's tiles were split
+    again = hip.attend(sc.kv, 0, q, hq, window=window)
+    hip.set_option("prefill_split", 0)
+    try:
+        whole = hip.attend(sc.kv, 0, q, hq, window=window)
+    finally:
+        hip.set_option("prefill_split", 1)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    for x in (got, whole):
+        err = np.abs(x - want).max()
+        assert close(x, want).all() and err < 2e-5, f"max abs err {err}"
+    assert np.abs(got - whole).max() < 2e-5
+    sc.kv.destroy()
+
+
 @pytest.mark.parametrize("hq,hkv,page,lens,k", [
     (16, 4, 16, [1, 300, 17, 64], 1), (8, 8, 16, [5, 40], 33), (32, 2, 128, [200, 1], 3),
     (16, 1, 16, [0, 1000], 2)])

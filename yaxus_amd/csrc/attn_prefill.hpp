@@ -43,9 +43,13 @@ struct PrefillItem {
   uint32_t r0;      // first pass row of the tile
   uint32_t nrows;   // rows (positions) in the tile
   uint32_t pt_off;  // the sequence's page table in the pass's pages
-  uint32_t blk0;    // first key block any row of the tile can see
-  uint32_t blk1;    // one past the last key block any row of the tile can see
-  uint32_t pad[3];
+  uint32_t blk0;    // first key block of this item's key range
+  uint32_t blk1;    // one past its last key block
+  // A tile whose keys are split over several items (a long context and too few tiles to
+  // fill the GPU): chunk index in bits 0-15, chunk count in bits 16-31 (1: not split).
+  uint32_t chunk_nch;
+  uint32_t part_base;  // partial slot of chunk 0 (split tiles)
+  uint32_t counter;    // arrival counter of the tile (split tiles)
 };
 
 static constexpr int kPrefillWaves = 4;
@@ -86,7 +90,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
     const uint32_t* __restrict__ pages, const _Float16* __restrict__ kc,
     const _Float16* __restrict__ vc, const float* q, float* __restrict__ out,
     uint32_t hq, uint32_t hkv, uint32_t bpp_shift, uint32_t window, float scale_log2,
-    QkvIn qi_in) {
+    QkvIn qi_in, float* __restrict__ part_o, float2* __restrict__ part_ml,
+    uint32_t* __restrict__ counters, uint32_t part_o_bytes, uint32_t part_ml_bytes) {
   constexpr int SB = SBT;
   static_assert(SB == 2 || SB == 4, "stages of one or two pairs of blocks");
   constexpr int PPS = SB / 2;  // pairs of 16-key blocks per stage
@@ -587,20 +592,56 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const size_t qd = static_cast<size_t>(hq) * kD;
+  const uint32_t nch = it.chunk_nch >> 16;
+  if (nch <= 1) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const float l = sum_xor32(sum_xor16(lsum[t]));
+      const uint32_t lr = (wave * NT + t) * 16 + c;
+      if (lr >= nlog) continue;
+      const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
+      // acc[t][j][i] is dim 16 j + 4 g + i of the column.
+      float* o = out + rr * qd + h * kD + g * 4;
+      const float inv = 1.0f / l;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        *reinterpret_cast<float4*>(o + j * 16) =
+            float4{acc[t][j][0] * inv, acc[t][j][1] * inv, acc[t][j][2] * inv, acc[t][j][3] * inv};
+    }
+    return;
+  }
+  // A split tile: this chunk's (maximum, sum, unnormalised O) of each column go to its
+  // partial slot (`[slot][kv head][kPrefillRows][128]`, device-coherent stores), and the
+  // tile's last chunk to arrive merges the chunks in chunk order (the split-K hand-off
+  // of the decode kernels, with the same memory-order argument).
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(part_o, part_o_bytes);
+  const __amdgpu_buffer_rsrc_t rml = make_rsrc(part_ml, part_ml_bytes);
+  const size_t slot = (static_cast<size_t>(it.part_base) + (it.chunk_nch & 0xffffu)) * hkv + kh;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const float l = sum_xor32(sum_xor16(lsum[t]));
     const uint32_t lr = (wave * NT + t) * 16 + c;
     if (lr >= nlog) continue;
-    const uint32_t rr = it.r0 + lr / G, h = kh * G + lr % G;
-    // acc[t][j][i] is dim 16 j + 4 g + i of the column.
-    float* o = out + rr * qd + h * kD + g * 4;
-    const float inv = 1.0f / l;
+    const size_t e = slot * kPrefillRows + lr;
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<float4*>(o + j * 16) =
-          float4{acc[t][j][0] * inv, acc[t][j][1] * inv, acc[t][j][2] * inv, acc[t][j][3] * inv};
+      st4_coherent(ro, static_cast<uint32_t>((e * kD + 16 * j + 4 * g) * 4),
+                   float4{acc[t][j][0], acc[t][j][1], acc[t][j][2], acc[t][j][3]});
+    if (g == 0) st2_coherent(rml, static_cast<uint32_t>(e * 8), float2{m[t], l});
   }
+  __builtin_amdgcn_s_waitcnt(0);
+  __shared__ uint32_t last_chunk;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t* cnt = counters + static_cast<size_t>(it.counter) * hkv + kh;
+    const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_chunk = arrived == nch - 1;
+    if (last_chunk) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last_chunk) return;
+  merge_group<64 * W, kPrefillRows>(it.r0, it.nrows, it.part_base, nch, 0u, 0u, 0u, kh, G, hq, hkv,
+                                    out, ro, rml);
 }
 
 }  // namespace yx

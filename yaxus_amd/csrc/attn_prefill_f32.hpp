@@ -38,7 +38,8 @@ __global__ __launch_bounds__(64 * kPf32Waves) __attribute__((amdgpu_waves_per_eu
     const PrefillItem* __restrict__ items, const uint32_t* pos,
     const uint32_t* __restrict__ pages, const float* __restrict__ kc, const float* __restrict__ vc,
     const float* q, float* __restrict__ out, uint32_t hq, uint32_t hkv, uint32_t bpp_shift,
-    uint32_t window, float scale_log2) {
+    uint32_t window, float scale_log2, float* __restrict__ part_o, float2* __restrict__ part_ml,
+    uint32_t* __restrict__ counters, uint32_t part_o_bytes, uint32_t part_ml_bytes) {
   // A ring of stages; each is 32 rows of 1 KiB: K of block b as rows 8b + t ([t][g][key c],
   // float4 = K[c][16t + 4g .. + 3]), then V of block b as rows 16 + 8b + 2t + h
   // ([t][h][g][c], float4 = V[4g + t][64h + 4c .. + 3]).
@@ -213,16 +214,47 @@ __global__ __launch_bounds__(64 * kPf32Waves) __attribute__((amdgpu_waves_per_eu
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const float l = sum_xor32(sum_xor16(lsum));
-  if (!has) return;
-  float* o = out + (static_cast<size_t>(rr) * hq + h) * kD;
-  const float inv = 1.0f / l;
+  const uint32_t nch = it.chunk_nch >> 16;
+  if (nch <= 1) {
+    if (!has) return;
+    float* o = out + (static_cast<size_t>(rr) * hq + h) * kD;
+    const float inv = 1.0f / l;
 #pragma unroll
-  for (int hh = 0; hh < 2; ++hh)
+    for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<float4*>(o + 64 * hh + 16 * g + 4 * i) =
-          float4{acc[4 * hh][i] * inv, acc[4 * hh + 1][i] * inv, acc[4 * hh + 2][i] * inv,
-                 acc[4 * hh + 3][i] * inv};
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float4*>(o + 64 * hh + 16 * g + 4 * i) =
+            float4{acc[4 * hh][i] * inv, acc[4 * hh + 1][i] * inv, acc[4 * hh + 2][i] * inv,
+                   acc[4 * hh + 3][i] * inv};
+    return;
+  }
+  // A split tile: partials and the last chunk's merge, as in the binary16 kernel.
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(part_o, part_o_bytes);
+  const __amdgpu_buffer_rsrc_t rml = make_rsrc(part_ml, part_ml_bytes);
+  if (has) {
+    const size_t slot = (static_cast<size_t>(it.part_base) + (it.chunk_nch & 0xffffu)) * hkv + kh;
+    const size_t e = slot * kPf32Rows + lr;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        st4_coherent(ro, static_cast<uint32_t>((e * kD + 64 * hh + 16 * g + 4 * i) * 4),
+                     float4{acc[4 * hh][i], acc[4 * hh + 1][i], acc[4 * hh + 2][i], acc[4 * hh + 3][i]});
+    if (g == 0) st2_coherent(rml, static_cast<uint32_t>(e * 8), float2{m, l});
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __shared__ uint32_t last_chunk;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t* cnt = counters + static_cast<size_t>(it.counter) * hkv + kh;
+    const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_chunk = arrived == nch - 1;
+    if (last_chunk) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last_chunk) return;
+  merge_group<64 * kPf32Waves, kPf32Rows>(it.r0, it.nrows, it.part_base, nch, 0u, 0u, 0u, kh, G, hq,
+                                          hkv, out, ro, rml);
 }
 
 }  // namespace yx

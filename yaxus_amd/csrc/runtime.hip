@@ -284,6 +284,7 @@ struct yx_ctx {
   std::vector<uint32_t> dev_mirror;              // what d_pages holds, entry by entry
   std::vector<std::tuple<size_t, size_t, size_t, bool, size_t>> used_keys;  // plans used this pass
   uint64_t pages_sent = 0, runs_sent = 0;        // page-table entries and runs uploaded (tests)
+  uint64_t split_tiles = 0;                       // prefill tiles split along keys (tests)
   bool have_pass = false;
   std::map<std::tuple<size_t, size_t, size_t, bool, size_t>, AttnPlan> plans;  // (window, hq, hkv, f32, page)
   // Work-list buffers of dropped plans, reused by the next pass's plans: a new pass
@@ -323,6 +324,7 @@ struct yx_ctx {
   // 2: the 16-row-tile kernel for every decode pass.
   long decode_shape = 0;
   long cascade = 1;  // attend keys shared by consecutive groups (same pages) once for all of them
+  long prefill_split = 1;  // split long prefill tiles along keys when the pass underfills the GPU
   bool profiling = false;
   Profile prof[4];
   bool capturing = false;
@@ -447,8 +449,52 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
         }
         w.blk0 = lo / 16;
         w.blk1 = hi / 16 + 1;
+        w.chunk_nch = 1u << 16;
         plan.pitems.push_back(w);
       }
+    // Tiles longer than 1.5 times the average load of a workgroup slot (two per CU; a
+    // long context with few tiles: one sequence's chunk after thousands of keys) are
+    // split along keys into chunks of about that load, at least kMinChunkPairs pairs of
+    // blocks each; the chunks' partial results are merged by the tile's last chunk.
+    // (cfg3's tiles, 1024 over 512 slots, stay whole.)
+    if (c->prefill_split) {
+      constexpr uint64_t kFixedPairs = 4;     // a tile's start and output, in pairs
+      constexpr uint32_t kMinChunkPairs = 16;
+      uint64_t total = 0;
+      for (const yx::PrefillItem& w : plan.pitems) total += (w.blk1 - w.blk0 + 1) / 2 + kFixedPairs;
+      total *= hkv;
+      // Workgroup slots: two per CU (4-wave binary16 tiles), one (8-wave f32 tiles).
+      const uint64_t slots2 = (f32 ? 1 : 2) * static_cast<uint64_t>(c->cus);
+      const uint64_t avg = std::max<uint64_t>(kMinChunkPairs, (total + slots2 - 1) / slots2);
+      std::vector<yx::PrefillItem> split;
+      uint32_t nslot = 0, ncnt = 0;
+      for (const yx::PrefillItem& w : plan.pitems) {
+        const uint32_t pairs = (w.blk1 - w.blk0 + 1) / 2;
+        uint32_t nch = 1;
+        if (2 * static_cast<uint64_t>(pairs) > 3 * avg)
+          nch = static_cast<uint32_t>(std::min<uint64_t>({(pairs + avg - 1) / avg, pairs / kMinChunkPairs, 64}));
+        if (nch <= 1) {
+          split.push_back(w);
+          continue;
+        }
+        for (uint32_t ch = 0; ch < nch; ++ch) {
+          yx::PrefillItem x = w;
+          // Chunk boundaries on pairs of blocks (the kernel's stage unit).
+          x.blk0 = w.blk0 + 2 * static_cast<uint32_t>(static_cast<uint64_t>(pairs) * ch / nch);
+          x.blk1 = ch + 1 == nch ? w.blk1 : w.blk0 + 2 * static_cast<uint32_t>(static_cast<uint64_t>(pairs) * (ch + 1) / nch);
+          x.chunk_nch = (nch << 16) | ch;
+          x.part_base = nslot;
+          x.counter = ncnt;
+          split.push_back(x);
+        }
+        nslot += nch;
+        ++ncnt;
+      }
+      plan.pitems = std::move(split);
+      plan.slots = nslot;
+      plan.counters = ncnt;
+      c->split_tiles += ncnt;
+    }
     // Longest first: the GPU hands work items to CUs in order as they free up, so
     // this bounds the busiest CU near the average (contexts differ a lot in a pass).
     std::stable_sort(plan.pitems.begin(), plan.pitems.end(),
@@ -781,7 +827,9 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
       c->used_keys.push_back(key);
   }
   // Logical rows per partial slot: the kernel's tile rows.
-  const size_t rps = plan->wide ? static_cast<size_t>((plan->nt + 1) / 2) * 16 : static_cast<size_t>(plan->nt) * 8;
+  const size_t rps = plan->prefill ? static_cast<size_t>(plan->f32 ? yx::kPf32Rows : yx::kPrefillRows)
+                    : plan->wide    ? static_cast<size_t>((plan->nt + 1) / 2) * 16
+                                    : static_cast<size_t>(plan->nt) * 8;
   const size_t po_need = plan->slots * hkv * rps * 128 * 4, pml_need = plan->slots * hkv * rps * 8;
   const size_t cnt_need = plan->counters * hkv * 4;
   const void* d_items;
@@ -848,6 +896,9 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     hipEvent_t e0;
     if ((rc = prof_begin(c, YX_KERNEL_ATTENTION, &e0))) return rc;
     const dim3 pgrid(static_cast<unsigned>(plan->pitems.size() * hkv));
+    if (po_cap > 0xffffffffu || pml_cap > 0xffffffffu)
+      return fail(YX_ERR_UNSUPPORTED, "prefill partials beyond 4 GiB");
+    const uint32_t pf_po_bytes = static_cast<uint32_t>(po_cap), pf_pml_bytes = static_cast<uint32_t>(pml_cap);
     if (plan->f32)
       hipLaunchKernelGGL(yx::paged_attn_prefill_f32, pgrid, dim3(64 * yx::kPf32Waves), 0, c->stream,
                          static_cast<const yx::PrefillItem*>(d_items), c->dev_pos,
@@ -855,21 +906,22 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
                          reinterpret_cast<const float*>(kv->k[layer]),
                          reinterpret_cast<const float*>(kv->v[layer]), q, out,
                          static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv), shift,
-                         static_cast<uint32_t>(window), scale * yx::kLog2e);
+                         static_cast<uint32_t>(window), scale * yx::kLog2e, po, pml, cnt,
+                         pf_po_bytes, pf_pml_bytes);
     else if (qkv)
       hipLaunchKernelGGL((yx::paged_attn_prefill<true>), pgrid, dim3(64 * yx::kPrefillWaves), 0, c->stream,
                        static_cast<const yx::PrefillItem*>(d_items),
                        c->dev_pos, static_cast<const uint32_t*>(c->d_pages.p),
                        kv->k[layer], kv->v[layer], q, out, static_cast<uint32_t>(hq),
                        static_cast<uint32_t>(hkv), shift, static_cast<uint32_t>(window),
-                       scale * yx::kLog2e, *qkv);
+                       scale * yx::kLog2e, *qkv, po, pml, cnt, pf_po_bytes, pf_pml_bytes);
     else
       hipLaunchKernelGGL((yx::paged_attn_prefill<false>), pgrid, dim3(64 * yx::kPrefillWaves), 0, c->stream,
                        static_cast<const yx::PrefillItem*>(d_items),
                        c->dev_pos, static_cast<const uint32_t*>(c->d_pages.p),
                        kv->k[layer], kv->v[layer], q, out, static_cast<uint32_t>(hq),
                        static_cast<uint32_t>(hkv), shift, static_cast<uint32_t>(window),
-                       scale * yx::kLog2e, yx::QkvIn{});
+                       scale * yx::kLog2e, yx::QkvIn{}, po, pml, cnt, pf_po_bytes, pf_pml_bytes);
     YX_HIP(hipGetLastError());
     return prof_end(c, YX_KERNEL_ATTENTION, e0);
   }
@@ -1080,10 +1132,11 @@ int yx_sync(yx_ctx* c) {
 int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
   if (!c || !key) return fail(YX_ERR_INVALID, "null argument");
   if (value < 0 || (value == 0 && std::strcmp(key, "attn_target_waves") &&
-                    std::strcmp(key, "attn_decode_shape") && std::strcmp(key, "attn_cascade")))
+                    std::strcmp(key, "attn_decode_shape") && std::strcmp(key, "attn_cascade") &&
+                    std::strcmp(key, "prefill_split")))
     return fail(YX_ERR_INVALID,
                 "option values are positive (attn_target_waves, attn_decode_shape: 0 = automatic; "
-                "attn_cascade: 0 = off)");
+                "attn_cascade, prefill_split: 0 = off)");
   if (!std::strcmp(key, "attn_target_waves"))
     c->target_waves = value;
   else if (!std::strcmp(key, "attn_max_tiles"))
@@ -1096,6 +1149,8 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
     c->max_chunk_blocks = value;
   else if (!std::strcmp(key, "attn_cascade"))
     c->cascade = value ? 1 : 0;
+  else if (!std::strcmp(key, "prefill_split"))
+    c->prefill_split = value ? 1 : 0;
   else
     return fail(YX_ERR_INVALID, std::string("unknown option ") + key);
   ++c->epoch;
@@ -1447,6 +1502,8 @@ int yx_ctx_get_stat(yx_ctx* c, const char* key, uint64_t* out) {
     *out = c->pages_sent;
   else if (!std::strcmp(key, "page_runs_sent"))
     *out = c->runs_sent;
+  else if (!std::strcmp(key, "prefill_split_tiles"))
+    *out = c->split_tiles;
   else
     return fail(YX_ERR_INVALID, std::string("unknown statistic ") + key);
   return YX_OK;
