@@ -310,7 +310,7 @@ def cfg5_pass(KvCache):
 
 def bench_configs(hip, steps=10, include_long=True, only=None):
     """Benchmark configurations 2-5 at full size (one JSON object per configuration);
-    `only`: a set of names among cfg2, cfg3, cfg4, cfg5, f32 to run (all when None)."""
+    `only`: a set of names among cfg2, cfg3, cfg4, cfg5, f32, long, step to run (all when None)."""
     from yaxus_amd import KvCache
     from yaxus_amd.data import uniform_ints
 
@@ -430,6 +430,30 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
                                            "f32_mfma_util_vs_157.3TF": round(flops / k_us / 1e6 / 157.3, 4),
                                            "split_k_decode_kernel_us": round(k_split, 2)}
         kv.destroy()
+    if want('long'):
+        # Chunked prefill of one long sequence (256 rows after 32768 keys): too few tiles
+        # to fill the GPU, so the prefill kernel splits them along keys; the same pass
+        # with the split off, for comparison (prefill kernel alone, HIP events).
+        pool = 2048 + 64
+        cache = KvCache(pool, 1 << 20, PAGE)
+        _scatter(cache, pool, SEED + 6)
+        s = cache.new_seq()
+        cache.append([(s, [1] * 32768)], [])
+        pr = cache.append([(s, [2] * 256)], [])
+        kv = hip.new_kv(4, pool, PAGE, HKV, D)
+        _fill_arena(hip, kv, 4, SEED + 6)
+        flops = 4 * HQ * D * (256 * 32768 + 256 * 257 // 2)
+        n = max(2, steps // 2)
+        k_split = _time_attention_kernel(hip, kv, pr, 4, HQ, n)
+        hip.set_option("prefill_split", 0)
+        k_whole = _time_attention_kernel(hip, kv, pr, 4, HQ, n)
+        hip.set_option("prefill_split", 1)
+        res["prefill_long_context"] = {"shape": "1 sequence, 256 rows after 32768 keys",
+                                       "attn_kernel_us": round(k_split, 2),
+                                       "TFLOPs": round(flops / k_split / 1e6, 1),
+                                       "attn_kernel_us_unsplit": round(k_whole, 2),
+                                       "flops_per_layer": flops}
+        kv.destroy()
     if want('step'):
         # The step after attention at the headline's decode shape: o_proj (16 rows of
         # hq * 128 = 2048 against a bf16 [2048][2048] weight) and the greedy pick over a
@@ -499,7 +523,7 @@ def main():
                     help="for rocprofv3: also run a 1 GiB device copy (the byte-counter "
                          "calibration point) and skip the CPU baseline")
     ap.add_argument("--only", default=None,
-                    help="with --configs: comma-separated subset of cfg2,cfg3,cfg4,cfg5,f32,step")
+                    help="with --configs: comma-separated subset of cfg2,cfg3,cfg4,cfg5,f32,long,step")
     ap.add_argument("--configs", action="store_true",
                     help="also measure benchmark configurations 2-5 at full size (adds ~2 min)")
     ap.add_argument("--no-graph", action="store_true",
