@@ -22,7 +22,10 @@
 // 5e-4 absolute against the f32 oracle, 1.3e-3 with q three times larger); K and V are
 // binary16 already. This doubles the MFMA work of the plain-f16 form. The tests compare
 // with the f32 oracle and an f64 brute force. Key pairs no column of a wave can see
-// (causal, window) are skipped by that wave.
+// (causal, window) are skipped by that wave. When a pass has too few tiles for the GPU
+// (one sequence's chunk after a long context), the host splits tiles along keys: each
+// chunk is its own work item, writes its columns' partial softmax, and the tile's last
+// chunk merges them in chunk order (merge_group, as the split-K decode kernels do).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
