@@ -294,6 +294,31 @@ def test_prefill_split_along_keys(hip, hq, hkv, page, window, prior, chunk, f32)
     sc.kv.destroy()
 
 
+def test_prefill_split_through_backend_attention(hip):
+    """Backend::attention in full (write_rows' key heads, then the prefill kernel, which
+    normalises and rotates its q heads itself) on a long sequence's chunk whose tiles
+    are split along keys: against write_rows + attention in the oracle."""
+    from yaxus_amd.rope import inv_freq, rope_table
+
+    hq, hkv = 16, 4
+    sc = Scenario(hip, pages=3200 // 16 + 16, page=16, hkv=hkv, pool_seed=9)
+    s = sc.cache.new_seq()
+    sc.prefill({s: 3000})
+    pr = sc.run_pass([(s, 64)])
+    rows = len(pr.meta.pos)
+    qkv = sc.draw(rows * (hq + 2 * hkv) * D).reshape(rows, -1)
+    qn, kn = sc.draw(D) * 0.1, sc.draw(D) * 0.1
+    f = inv_freq(D, 10000.0)
+    split0 = hip.stat("prefill_split_tiles")
+    got = hip.attention(sc.kv, 0, qkv, qn, kn, rope_table(f, 1.0, 4096), 1e-6, hq)
+    assert hip.stat("prefill_split_tiles") > split0
+    qo = sc.orc[0].write_rows(qkv, hq, qn, kn, 1e-6, f, 1.0, pr.meta.pos, pr.meta.kv_slot)
+    want = sc.orc[0].attend(qo, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
+    err = np.abs(got - want).max()
+    assert close(got, want).all() and err < 2e-5, f"max abs err {err}"
+    sc.kv.destroy()
+
+
 @pytest.mark.parametrize("hq,hkv,page,lens,k", [
     (16, 4, 16, [1, 300, 17, 64], 1), (8, 8, 16, [5, 40], 33), (32, 2, 128, [200, 1], 3),
     (16, 1, 16, [0, 1000], 2)])
