@@ -25,7 +25,8 @@
 // (causal, window) are skipped by that wave. When a pass has too few tiles for the GPU
 // (one sequence's chunk after a long context), the host splits tiles along keys: each
 // chunk is its own work item, writes its columns' partial softmax, and the tile's last
-// chunk merges them in chunk order (merge_group, as the split-K decode kernels do).
+// chunk merges them in chunk order (merge_tile; the hand-off of the split-K decode
+// kernels).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -54,6 +55,71 @@ struct PrefillItem {
   uint32_t part_base;  // partial slot of chunk 0 (split tiles)
   uint32_t counter;    // arrival counter of the tile (split tiles)
 };
+
+// Merges a split tile's chunks (the tile's last chunk does it): the partial (maximum,
+// sum, unnormalised O) of each logical row in chunk slots base .. base + nch - 1, in
+// chunk order, so the result does not depend on arrival order. A thread takes kPer
+// (row, 4 dims) entries, kGE at a time, and has the loads of kCB chunks of those kGE
+// entries in flight at once (a tile's partials are many: 64 or 128 rows per chunk).
+template <int kThreads, int kRows>
+__device__ __forceinline__ void merge_tile(uint32_t r0, uint32_t nrows, uint32_t base, uint32_t nch,
+                                           uint32_t kh, uint32_t G, uint32_t hq, uint32_t hkv,
+                                           float* __restrict__ out, __amdgpu_buffer_rsrc_t ro,
+                                           __amdgpu_buffer_rsrc_t rml) {
+  constexpr int kPer = kRows * 32 / kThreads;
+  constexpr int kGE = 4, kCB = 4;
+  static_assert(kPer % kGE == 0, "whole groups of entries per thread");
+  const uint32_t nlog = nrows * G;
+  const size_t qd = static_cast<size_t>(hq) * kD;
+#pragma unroll
+  for (int e0 = 0; e0 < kPer; e0 += kGE) {
+    float mt[kGE], lt[kGE];
+    float4 o[kGE];
+    uint32_t lr[kGE], qi[kGE];
+#pragma unroll
+    for (int j = 0; j < kGE; ++j) {
+      const uint32_t idx = threadIdx.x + (e0 + j) * kThreads;
+      lr[j] = idx >> 5;
+      qi[j] = idx & 31;
+      mt[j] = -INFINITY;
+      lt[j] = 0.0f;
+      o[j] = float4{0, 0, 0, 0};
+    }
+    for (uint32_t c0 = 0; c0 < nch; c0 += kCB) {
+      float2 ml[kGE][kCB];
+      float4 po[kGE][kCB];
+#pragma unroll
+      for (int j = 0; j < kGE; ++j)
+#pragma unroll
+        for (int b = 0; b < kCB; ++b) {
+          const uint32_t ch = min(c0 + b, nch - 1);
+          const size_t e = ((static_cast<size_t>(base) + ch) * hkv + kh) * kRows + (lr[j] < nlog ? lr[j] : 0u);
+          ml[j][b] = ld2_coherent(rml, static_cast<uint32_t>(e * 8));
+          po[j][b] = ld4_coherent(ro, static_cast<uint32_t>((e * kD + qi[j] * 4) * 4));
+        }
+#pragma unroll
+      for (int j = 0; j < kGE; ++j)
+#pragma unroll
+        for (int b = 0; b < kCB; ++b) {
+          if (c0 + b >= nch || !(ml[j][b].y > 0.0f)) continue;  // past the list, or empty
+          const float mn = fmaxf(mt[j], ml[j][b].x);
+          const float r = __builtin_amdgcn_exp2f(mt[j] - mn), wt = __builtin_amdgcn_exp2f(ml[j][b].x - mn);
+          lt[j] = lt[j] * r + ml[j][b].y * wt;
+          o[j] = float4{o[j].x * r + po[j][b].x * wt, o[j].y * r + po[j][b].y * wt,
+                        o[j].z * r + po[j][b].z * wt, o[j].w * r + po[j][b].w * wt};
+          mt[j] = mn;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kGE; ++j) {
+      if (lr[j] >= nlog) continue;
+      const uint32_t rr = r0 + lr[j] / G, h = kh * G + lr[j] % G;
+      const float inv = 1.0f / lt[j];
+      *reinterpret_cast<float4*>(out + rr * qd + h * kD + qi[j] * 4) =
+          float4{o[j].x * inv, o[j].y * inv, o[j].z * inv, o[j].w * inv};
+    }
+  }
+}
 
 static constexpr int kPrefillWaves = 4;
 static constexpr int kPrefillTiles = 1;  // MFMA tiles (16 logical rows) per wave
@@ -616,7 +682,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   // A split tile: this chunk's (maximum, sum, unnormalised O) of each column go to its
   // partial slot (`[slot][kv head][kPrefillRows][128]`, device-coherent stores), and the
   // tile's last chunk to arrive merges the chunks in chunk order (the split-K hand-off
-  // of the decode kernels, with the same memory-order argument).
+  // of the decode kernels, with the same memory-order argument; merge_tile).
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(part_o, part_o_bytes);
   const __amdgpu_buffer_rsrc_t rml = make_rsrc(part_ml, part_ml_bytes);
   const size_t slot = (static_cast<size_t>(it.part_base) + (it.chunk_nch & 0xffffu)) * hkv + kh;
@@ -643,8 +709,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   }
   __syncthreads();
   if (!last_chunk) return;
-  merge_group<64 * W, kPrefillRows>(it.r0, it.nrows, it.part_base, nch, 0u, 0u, 0u, kh, G, hq, hkv,
-                                    out, ro, rml);
+  merge_tile<64 * W, kPrefillRows>(it.r0, it.nrows, it.part_base, nch, kh, G, hq, hkv, out, ro, rml);
 }
 
 }  // namespace yx

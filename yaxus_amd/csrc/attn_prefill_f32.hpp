@@ -253,8 +253,7 @@ __global__ __launch_bounds__(64 * kPf32Waves) __attribute__((amdgpu_waves_per_eu
   }
   __syncthreads();
   if (!last_chunk) return;
-  merge_group<64 * kPf32Waves, kPf32Rows>(it.r0, it.nrows, it.part_base, nch, 0u, 0u, 0u, kh, G, hq,
-                                          hkv, out, ro, rml);
+  merge_tile<64 * kPf32Waves, kPf32Rows>(it.r0, it.nrows, it.part_base, nch, kh, G, hq, hkv, out, ro, rml);
 }
 
 }  // namespace yx
