@@ -423,7 +423,7 @@ def bench_configs(hip, steps=10, include_long=True, only=None):
         k_us = _time_attention_kernel(hip, kv, pr, layers, HQ, n)
         hip.set_option("prefill_min_rows", 1 << 20)
         k_split = _time_attention_kernel(hip, kv, pr, layers, HQ, n)
-        hip.set_option("prefill_min_rows", 32)
+        hip.set_option("prefill_min_rows", 0)
         flops = sum(4 * HQ * D * (256 * p + 256 * 257 // 2) for p in prior)
         res["cfg3_chunked_prefill_f32"] = {"attn_kernel_us": round(k_us, 2),
                                            "TFLOPs": round(flops / k_us / 1e6, 2),

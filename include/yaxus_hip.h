@@ -55,7 +55,10 @@ int yx_sync(yx_ctx* ctx);
  * one decode work item holds, 1-4, default 4; 3 at most with attn_decode_shape 1 unless
  * one row's q heads need 4, which then take the 16-row-tile kernel; a row's q heads
  * always fit one work item),
- * "prefill_min_rows" (rows of one sequence from which the prefill kernel is used),
+ * "prefill_min_rows" (rows of one sequence from which the prefill kernel is used; 0,
+ * the default: automatic, the prefill kernel when a sequence has more (row, q head)
+ * pairs than one decode work item holds and the pass makes at least one prefill tile
+ * per 8 CUs, 32 rows on the f32 arena),
  * "attn_decode_shape" (0, the default: automatic. Passes of more than 8 logical rows per
  * work item use the kernel with 16-row tiles and a fixed split of blocks over its waves;
  * so do one-tile passes whose work items split evenly over the waves or hold more than
@@ -68,8 +71,8 @@ int yx_sync(yx_ctx* ctx);
  * prefill tiles much longer than the average load of a workgroup slot, e.g. a chunk of
  * one long sequence, are split along keys and their partial results merged; 0: every
  * tile is one work item). Setting an option drops cached work lists. Values are
- * positive; 0 is accepted for attn_target_waves, attn_decode_shape, attn_cascade and
- * prefill_split. */
+ * positive; 0 is accepted for attn_target_waves, attn_decode_shape, attn_cascade,
+ * prefill_split and prefill_min_rows. */
 int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
 /* Counters of the context since its creation: "page_entries_sent" (page-table entries
  * yx_pass_begin uploaded), "page_runs_sent" (runs of consecutive entries they formed)

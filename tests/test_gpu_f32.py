@@ -153,7 +153,7 @@ def test_f32_prefill_tiles_match_oracle(hip, hq, hkv, page, window, chunk):
     assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
     exact = sc.orc[0].attend_f64(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
     assert np.abs(got - exact).max() < 1e-5
-    with _option(hip, "prefill_min_rows", 1 << 20, 32):
+    with _option(hip, "prefill_min_rows", 1 << 20, 0):
         split = hip.attend(sc.kv, 0, q, hq, window=window)
     assert np.abs(got - split).max() < 1e-5
     sc.kv.destroy()

@@ -277,15 +277,19 @@ def test_prefill_split_along_keys(hip, hq, hkv, page, window, prior, chunk, f32)
     rows = len(pr.meta.pos)
     q = sc.draw(rows * hq * D).reshape(rows, hq * D)
     want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
-    split0 = hip.stat("prefill_split_tiles")
-    got = hip.attend(sc.kv, 0, q, hq, window=window)
-    assert hip.stat("prefill_split_tiles") > split0  # the long sequence's tiles were split
-    again = hip.attend(sc.kv, 0, q, hq, window=window)
-    hip.set_option("prefill_split", 0)
+    hip.set_option("prefill_min_rows", 1)  # the prefill kernel (few tiles: decode by default)
     try:
-        whole = hip.attend(sc.kv, 0, q, hq, window=window)
+        split0 = hip.stat("prefill_split_tiles")
+        got = hip.attend(sc.kv, 0, q, hq, window=window)
+        assert hip.stat("prefill_split_tiles") > split0  # the long sequence's tiles were split
+        again = hip.attend(sc.kv, 0, q, hq, window=window)
+        hip.set_option("prefill_split", 0)
+        try:
+            whole = hip.attend(sc.kv, 0, q, hq, window=window)
+        finally:
+            hip.set_option("prefill_split", 1)
     finally:
-        hip.set_option("prefill_split", 1)
+        hip.set_option("prefill_min_rows", 0)
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
     for x in (got, whole):
         err = np.abs(x - want).max()
@@ -309,9 +313,13 @@ def test_prefill_split_through_backend_attention(hip):
     qkv = sc.draw(rows * (hq + 2 * hkv) * D).reshape(rows, -1)
     qn, kn = sc.draw(D) * 0.1, sc.draw(D) * 0.1
     f = inv_freq(D, 10000.0)
-    split0 = hip.stat("prefill_split_tiles")
-    got = hip.attention(sc.kv, 0, qkv, qn, kn, rope_table(f, 1.0, 4096), 1e-6, hq)
-    assert hip.stat("prefill_split_tiles") > split0
+    hip.set_option("prefill_min_rows", 1)  # the prefill kernel (few tiles: decode by default)
+    try:
+        split0 = hip.stat("prefill_split_tiles")
+        got = hip.attention(sc.kv, 0, qkv, qn, kn, rope_table(f, 1.0, 4096), 1e-6, hq)
+        assert hip.stat("prefill_split_tiles") > split0
+    finally:
+        hip.set_option("prefill_min_rows", 0)
     qo = sc.orc[0].write_rows(qkv, hq, qn, kn, 1e-6, f, 1.0, pr.meta.pos, pr.meta.kv_slot)
     want = sc.orc[0].attend(qo, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
     err = np.abs(got - want).max()

@@ -44,7 +44,7 @@ def test_tiled_attention_matches_per_row_and_cpu(hip, f32):
     q = sc.draw(40 * HQ * D).reshape(40, HQ * D)
     want = sc.orc[0].attend(q, HQ, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
     tiled = hip.attend(sc.kv, 0, q, HQ)                       # prefill kernel (40 rows >= 32)
-    with _opt(hip, "prefill_min_rows", 1 << 20, 32):
+    with _opt(hip, "prefill_min_rows", 1 << 20, 0):
         per_row = hip.attend(sc.kv, 0, q, HQ)                 # split-K decode kernel
         with _opt(hip, "attn_target_waves", 1 << 14, 0):
             split = hip.attend(sc.kv, 0, q, HQ)               # the keys split finer

@@ -315,7 +315,7 @@ struct yx_ctx {
   long target_waves = 0;  // 0: one work item per CU
   int cus = 256;
   long max_chunk_blocks = 1 << 20;
-  long prefill_min_rows = 32;
+  long prefill_min_rows = 0;  // 0: automatic (see build_plan)
   // Most 8-row units of logical rows per work item. The wide kernel holds 32 rows in two
   // 16-row tiles; the static 8-row-tile kernel spills with a fourth tile, so it keeps 3
   // unless one row's q heads need 4.
@@ -425,7 +425,27 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
   const size_t G = hq / hkv;
   uint32_t max_rows = 0;
   for (const Group& g : c->groups) max_rows = std::max(max_rows, g.n);
-  if (max_rows >= static_cast<uint32_t>(c->prefill_min_rows)) {
+  // Prefill tiles or split-K decode items. With a fixed threshold (option
+  // prefill_min_rows > 0), by rows of one sequence. Automatically (0, the default): the
+  // prefill kernel when a sequence has more logical rows than one decode work item holds
+  // (the decode kernels would read its keys once per item) and the pass makes at least
+  // one prefill tile per 8 CUs (with fewer, its tiles split into chunks too short to pay
+  // for their merge: one sequence of 32-64 rows after 4096-32768 keys runs 1.2-2x faster
+  // as decode items); the f32 arena keeps a 32-row threshold. Measured (B x rows after
+  // ctx, decode / prefill us): 16 x 10 after 4096 57.1 / 49.5, 16 x 8 34.2 / 43.0, 1 x 32
+  // after 32768 50.1 / 101.1, 1 x 128 after 32768 218.1 / 103.6, 2 x 64 after 16384
+  // 81.5 / 70.7.
+  bool use_prefill;
+  if (c->prefill_min_rows > 0 || f32) {
+    use_prefill = max_rows >= static_cast<uint32_t>(c->prefill_min_rows > 0 ? c->prefill_min_rows : 32);
+  } else {
+    size_t tiles = 0;
+    for (const Group& g : c->groups) tiles += (g.n * G + yx::kPrefillRows - 1) / yx::kPrefillRows;
+    tiles *= hkv;
+    use_prefill = max_rows * G > static_cast<size_t>(c->max_tiles) * 8 &&
+                  tiles * 8 >= static_cast<size_t>(c->cus);
+  }
+  if (use_prefill) {
     // Tiles of kPrefillRows logical rows: consecutive rows of one sequence (the f16 and
     // the f32 arena's prefill kernels take the same items).
     AttnPlan plan;
@@ -1133,10 +1153,10 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
   if (!c || !key) return fail(YX_ERR_INVALID, "null argument");
   if (value < 0 || (value == 0 && std::strcmp(key, "attn_target_waves") &&
                     std::strcmp(key, "attn_decode_shape") && std::strcmp(key, "attn_cascade") &&
-                    std::strcmp(key, "prefill_split")))
+                    std::strcmp(key, "prefill_split") && std::strcmp(key, "prefill_min_rows")))
     return fail(YX_ERR_INVALID,
-                "option values are positive (attn_target_waves, attn_decode_shape: 0 = automatic; "
-                "attn_cascade, prefill_split: 0 = off)");
+                "option values are positive (attn_target_waves, attn_decode_shape, prefill_min_rows: "
+                "0 = automatic; attn_cascade, prefill_split: 0 = off)");
   if (!std::strcmp(key, "attn_target_waves"))
     c->target_waves = value;
   else if (!std::strcmp(key, "attn_max_tiles"))
