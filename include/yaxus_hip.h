@@ -58,7 +58,8 @@ int yx_sync(yx_ctx* ctx);
  * "prefill_min_rows" (rows of one sequence from which the prefill kernel is used; 0,
  * the default: automatic, the prefill kernel when a sequence has more (row, q head)
  * pairs than one decode work item holds and the pass makes at least one prefill tile
- * per 8 CUs, 32 rows on the f32 arena),
+ * per 8 CUs; on the f32 arena, the kernel with the smaller time estimated from the
+ * keys its decode items would read, the longest context and the pass's products),
  * "attn_decode_shape" (0, the default: automatic. Passes of more than 8 logical rows per
  * work item use the kernel with 16-row tiles and a fixed split of blocks over its waves;
  * so do one-tile passes whose work items split evenly over the waves or hold more than
@@ -76,7 +77,8 @@ int yx_sync(yx_ctx* ctx);
 int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
 /* Counters of the context since its creation: "page_entries_sent" (page-table entries
  * yx_pass_begin uploaded), "page_runs_sent" (runs of consecutive entries they formed)
- * and "prefill_split_tiles" (prefill tiles split along keys in the work lists built).
+ * "prefill_split_tiles" (prefill tiles split along keys in the work lists built) and
+ * "prefill_plans" (work lists built as prefill tiles rather than decode items).
  * A pass whose groups keep their order and fit the device regions of the previous pass
  * sends only the entries that changed. */
 int yx_ctx_get_stat(yx_ctx* ctx, const char* key, uint64_t* out);
@@ -84,9 +86,9 @@ int yx_ctx_get_stat(yx_ctx* ctx, const char* key, uint64_t* out);
 /* Backend::new_kv (lib.rs:118; GPU ops/mod.rs:42-66): `layers` layers of `pages`
  * pages of `page_size` tokens (a multiple of 16), zeroed. dtype YX_DTYPE_F16 (binary16,
  * the fast path) or YX_DTYPE_F32 (the reference's own K/V precision: stores are exact,
- * attention runs on f32 MFMAs, every pass as split-K decode with at most 16 (row, q
- * head) pairs per work item, at most 16 q heads per KV head, write_rows as its own
- * launch). */
+ * attention runs on f32 MFMAs: split-K decode items of at most 16 (row, q head) pairs,
+ * or prefill tiles of 128, chosen by the prefill_min_rows option of yx_ctx_set_option;
+ * at most 16 q heads per KV head; write_rows as its own launch). */
 int yx_kv_create(yx_ctx* ctx, size_t layers, size_t pages, size_t page_size, size_t hkv,
                  size_t head_dim, int dtype, yx_kv** out);
 int yx_kv_destroy(yx_ctx* ctx, yx_kv* kv);

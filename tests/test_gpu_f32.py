@@ -61,6 +61,15 @@ def test_f32_decode_and_verify_match_oracle(hip, hq, hkv, page, window, k):
     sc.kv.destroy()
 
 
+@pytest.fixture(autouse=True)
+def _prefill_from_32_rows(hip):
+    """The prefill kernel for every pass with 32 or more rows of one sequence (the
+    automatic choice would attend these small passes as decode items)."""
+    hip.set_option("prefill_min_rows", 32)
+    yield
+    hip.set_option("prefill_min_rows", 0)
+
+
 @contextlib.contextmanager
 def _option(hip, key, value, default):
     hip.set_option(key, value)
@@ -153,7 +162,7 @@ def test_f32_prefill_tiles_match_oracle(hip, hq, hkv, page, window, chunk):
     assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
     exact = sc.orc[0].attend_f64(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
     assert np.abs(got - exact).max() < 1e-5
-    with _option(hip, "prefill_min_rows", 1 << 20, 0):
+    with _option(hip, "prefill_min_rows", 1 << 20, 32):
         split = hip.attend(sc.kv, 0, q, hq, window=window)
     assert np.abs(got - split).max() < 1e-5
     sc.kv.destroy()

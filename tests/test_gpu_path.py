@@ -249,7 +249,13 @@ def test_prefill_tiles_match_oracle(hip, hq, hkv, page, window, chunk):
     kk = sc.draw(rows * hkv * D).reshape(rows, hkv, D)
     vv = sc.draw(rows * hkv * D).reshape(rows, hkv, D)
     q = sc.draw(rows * hq * D).reshape(rows, hq * D)
-    got = hip.attend_append(sc.kv, 0, kk, vv, q, hq, window=window)
+    before = hip.stat("prefill_plans")
+    hip.set_option("prefill_min_rows", 1)  # the tile kernel whatever the automatic choice
+    try:
+        got = hip.attend_append(sc.kv, 0, kk, vv, q, hq, window=window)
+    finally:
+        hip.set_option("prefill_min_rows", 0)
+    assert hip.stat("prefill_plans") == before + 1
     sc.orc[0].store(pr.meta.kv_slot, kk.reshape(rows, -1), vv.reshape(rows, -1))
     want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
     err = np.abs(got - want).max()
@@ -420,23 +426,27 @@ def test_model_attention_two_passes_across_pages(hip, window):
     kv.destroy()
 
 
-@pytest.mark.parametrize("hq,hkv,lens,k", [
-    (16, 4, [1, 300, 17, 1000, 64], 1), (8, 2, [40, 513], 1), (16, 4, [40, 513, 7], 5),
-    (32, 2, [100, 2000], 1), (16, 4, [40, 513, 7], 40), (8, 8, [0, 130], 70),
-    (16, 4, [4095], 1), (16, 4, [40, 513, 7], 4)])
-def test_attention_in_one_launch_equals_two(hip, hq, hkv, lens, k):
+@pytest.mark.parametrize("hq,hkv,lens,k,min_rows", [
+    (16, 4, [1, 300, 17, 1000, 64], 1, 0), (8, 2, [40, 513], 1, 0), (16, 4, [40, 513, 7], 5, 0),
+    (32, 2, [100, 2000], 1, 0), (16, 4, [40, 513, 7], 40, 0), (8, 8, [0, 130], 70, 0),
+    (16, 4, [40, 513, 7], 40, 32), (8, 8, [0, 130], 70, 32),
+    (16, 4, [4095], 1, 0), (16, 4, [40, 513, 7], 4, 0)])
+def test_attention_in_one_launch_equals_two(hip, request, hq, hkv, lens, k, min_rows):
     """Backend::attention in full gives the same bits (attention output and stored K/V)
     as write_rows then attention as separate calls, and both match the oracle: decode
     passes in one launch (the decode kernel runs write_rows itself: the queue kernel, or
     the 16-row-tile kernel for [4095], whose 8-quad work items split evenly over its
     waves, and for k = 4, 16 logical rows), verify passes of more rows (k = 5) as
-    write_rows then attention, prefill passes (k >= 32) as the key heads' write_rows
-    then the prefill kernel, which normalises and rotates its q heads itself."""
+    write_rows then attention, prefill passes (k >= 32 with min_rows 32; automatically
+    these few tiles are decode items) as the key heads' write_rows then the prefill
+    kernel, which normalises and rotates its q heads itself."""
     from yaxus_amd.rope import inv_freq, rope_table
 
     f = inv_freq(D, 10000.0)
     table = rope_table(f, 1.0, 4096)
     outs, scs = [], []
+    hip.set_option("prefill_min_rows", min_rows)
+    request.addfinalizer(lambda: hip.set_option("prefill_min_rows", 0))
     for one_launch in (True, False):
         sc = Scenario(hip, pages=400, page=16, hkv=hkv, pool_seed=21)
         seqs = [sc.cache.new_seq() for _ in lens]

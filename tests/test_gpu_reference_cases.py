@@ -43,11 +43,15 @@ def test_tiled_attention_matches_per_row_and_cpu(hip, f32):
     k, v = sc.store(pr)
     q = sc.draw(40 * HQ * D).reshape(40, HQ * D)
     want = sc.orc[0].attend(q, HQ, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
-    tiled = hip.attend(sc.kv, 0, q, HQ)                       # prefill kernel (40 rows >= 32)
+    with _opt(hip, "prefill_min_rows", 1, 0):
+        tiled = hip.attend(sc.kv, 0, q, HQ)                   # prefill kernel
     with _opt(hip, "prefill_min_rows", 1 << 20, 0):
         per_row = hip.attend(sc.kv, 0, q, HQ)                 # split-K decode kernel
         with _opt(hip, "attn_target_waves", 1 << 14, 0):
             split = hip.attend(sc.kv, 0, q, HQ)               # the keys split finer
+    before = hip.stat("prefill_plans")
+    hip.attend(sc.kv, 0, q, HQ)
+    assert hip.stat("prefill_plans") == before, "one 40-row chunk: decode items by default"
     for name, got in (("tiled", tiled), ("per-row", per_row), ("split keys", split)):
         err = np.abs(got - want).max()
         assert close(got, want).all(), f"{name}: max |gpu - cpu| = {err:.2e}"

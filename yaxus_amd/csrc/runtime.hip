@@ -285,6 +285,7 @@ struct yx_ctx {
   std::vector<std::tuple<size_t, size_t, size_t, bool, size_t>> used_keys;  // plans used this pass
   uint64_t pages_sent = 0, runs_sent = 0;        // page-table entries and runs uploaded (tests)
   uint64_t split_tiles = 0;                       // prefill tiles split along keys (tests)
+  uint64_t prefill_plans = 0;                     // work lists built as prefill tiles (tests)
   bool have_pass = false;
   std::map<std::tuple<size_t, size_t, size_t, bool, size_t>, AttnPlan> plans;  // (window, hq, hkv, f32, page)
   // Work-list buffers of dropped plans, reused by the next pass's plans: a new pass
@@ -431,13 +432,40 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
   // (the decode kernels would read its keys once per item) and the pass makes at least
   // one prefill tile per 8 CUs (with fewer, its tiles split into chunks too short to pay
   // for their merge: one sequence of 32-64 rows after 4096-32768 keys runs 1.2-2x faster
-  // as decode items); the f32 arena keeps a 32-row threshold. Measured (B x rows after
+  // as decode items). Measured (B x rows after
   // ctx, decode / prefill us): 16 x 10 after 4096 57.1 / 49.5, 16 x 8 34.2 / 43.0, 1 x 32
   // after 32768 50.1 / 101.1, 1 x 128 after 32768 218.1 / 103.6, 2 x 64 after 16384
   // 81.5 / 70.7.
   bool use_prefill;
-  if (c->prefill_min_rows > 0 || f32) {
-    use_prefill = max_rows >= static_cast<uint32_t>(c->prefill_min_rows > 0 ? c->prefill_min_rows : 32);
+  if (c->prefill_min_rows > 0) {
+    use_prefill = max_rows >= static_cast<uint32_t>(c->prefill_min_rows);
+  } else if (f32) {
+    // The f32 arena: its decode items hold 16 logical rows each and re-read their
+    // sequence's keys once per item (about 6 TB/s over those reads); its prefill tiles
+    // (128 logical rows, one workgroup per CU) take about 95 us plus 2.4 us per 1024 keys
+    // of the longest context (the key split's chain), or 40 us plus their products at
+    // 110 TFLOP/s, whichever is more. The kernel with the smaller estimate runs. Measured
+    // (B x rows after ctx, decode / prefill us; the choice was right in 19 of 21 shapes,
+    // the two misses 5% and 30%): 1 x 32 after 4096 32.6 / 101.8, 1 x 128 after 4096
+    // 83.9 / 107.2, 32 x 8 after 2048 94.8 / 119.2, 1 x 48 after 16384 186.6 / 133.4,
+    // 1 x 96 after 8192 197.4 / 118.9, 4 x 32 after 8192 177.6 / 129.5, 16 x 10 after
+    // 4096 172.0 / 127.6, 1 x 32 after 32768 137.7 / 178.7, 1 x 64 after 32768
+    // 453.3 / 217.3, 16 x 256 after 1024 812.5 / 352.8.
+    double decode_bytes = 0, flops = 0;
+    uint32_t max_keys = 0;
+    for (const Group& g : c->groups) {
+      uint32_t keys = 0;
+      for (uint32_t i = g.r0; i < g.r0 + g.n; ++i) keys = std::max(keys, c->pos[i] + 1);
+      if (window > 0) keys = static_cast<uint32_t>(std::min<uint64_t>(keys, window + g.n));
+      max_keys = std::max(max_keys, keys);
+      decode_bytes += static_cast<double>((g.n * G + 15) / 16) * keys;
+      flops += static_cast<double>(g.n) * G * keys;
+    }
+    decode_bytes *= static_cast<double>(hkv) * yx::kD * sizeof(float) * 2;
+    flops *= static_cast<double>(hkv) * 4 * yx::kD;
+    const double decode_us = decode_bytes / 6e6;
+    const double prefill_us = std::max(95.0 + 2.4 * max_keys / 1024.0, 40.0 + flops / 1.1e8);
+    use_prefill = max_rows * G > 16 && decode_us > prefill_us;
   } else {
     size_t tiles = 0;
     for (const Group& g : c->groups) tiles += (g.n * G + yx::kPrefillRows - 1) / yx::kPrefillRows;
@@ -446,6 +474,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
                   tiles * 8 >= static_cast<size_t>(c->cus);
   }
   if (use_prefill) {
+    ++c->prefill_plans;
     // Tiles of kPrefillRows logical rows: consecutive rows of one sequence (the f16 and
     // the f32 arena's prefill kernels take the same items).
     AttnPlan plan;
@@ -1524,6 +1553,8 @@ int yx_ctx_get_stat(yx_ctx* c, const char* key, uint64_t* out) {
     *out = c->runs_sent;
   else if (!std::strcmp(key, "prefill_split_tiles"))
     *out = c->split_tiles;
+  else if (!std::strcmp(key, "prefill_plans"))
+    *out = c->prefill_plans;
   else
     return fail(YX_ERR_INVALID, std::string("unknown statistic ") + key);
   return YX_OK;
