@@ -71,9 +71,13 @@ int yx_sync(yx_ctx* ctx);
  * row's own; 0: every group reads its whole context). "prefill_split" (1, the default:
  * prefill tiles much longer than the average load of a workgroup slot, e.g. a chunk of
  * one long sequence, are split along keys and their partial results merged; 0: every
- * tile is one work item). Setting an option drops cached work lists. Values are
- * positive; 0 is accepted for attn_target_waves, attn_decode_shape, attn_cascade,
- * prefill_split and prefill_min_rows. */
+ * tile is one work item). "matmul_k_split" (workgroups per yx_matmul_bf16_dev output
+ * tile along k, at most 64; 0, the default: automatic) and "argmax_slices" (workgroups
+ * per yx_argmax_rows_dev row, at most 1024; 0, the default: automatic); neither changes
+ * argmax's result, and matmul's only by the order of its f32 additions. Setting an
+ * option drops cached work lists. Values are positive; 0 is accepted for
+ * attn_target_waves, attn_decode_shape, attn_cascade, prefill_split, prefill_min_rows,
+ * matmul_k_split and argmax_slices. */
 int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
 /* Counters of the context since its creation: "page_entries_sent" (page-table entries
  * yx_pass_begin uploaded), "page_runs_sent" (runs of consecutive entries they formed)
@@ -170,7 +174,8 @@ int yx_attention_append_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k
 /* No counterpart in the reference: yx_attention_append_dev for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). Same kernels, arguments and results; the split-K work list, partials and
- * arrival counters live in the library's static device scratch (16 MiB per GPU, held
+ * arrival counters live in the library's static device scratch (16 MiB per GPU, of
+ * which 1 MiB holds 8192 counters, one per 128-byte line; held
  * until the process ends) instead of buffers of the context, so the call makes no
  * device or pinned-host allocation (the pass's pinned staging from yx_pass_begin must
  * hold the work list). A pass whose work list and partials do not fit the scratch is

@@ -113,3 +113,48 @@ def test_argmax_handles_a_whole_pass(hip, rows):
         got.free()
     finally:
         d.free()
+
+
+@pytest.mark.parametrize("slices", [1, 3, 19, 152, 1024])
+def test_argmax_result_does_not_depend_on_the_slices(hip, slices):
+    """The option argmax_slices (workgroups per row): every count gives the CPU's pick,
+    ties across slices included; then back to the automatic count."""
+    rng = np.random.default_rng(slices)
+    logits = rng.standard_normal((16, 151936), dtype=np.float32)
+    logits[0, [3, 151000]] = 50.0
+    logits[1, :] = np.nan
+    logits[2, 100000:] = 7.0
+    d = hip.tensor(logits.shape).upload(logits)
+    hip.set_option("argmax_slices", slices)
+    try:
+        for _ in range(2):  # the counters are back at zero for the next call
+            got = hip.argmax_rows(d)
+            np.testing.assert_array_equal(got.numpy(), argmax_rows(logits))
+            got.free()
+    finally:
+        hip.set_option("argmax_slices", 0)
+        d.free()
+
+
+@pytest.mark.parametrize("ks", [1, 2, 5, 16, 64])
+def test_matmul_k_split_stays_within_the_bound(hip, ks):
+    """The option matmul_k_split (workgroups per output tile along k): each split is
+    within the f32 accumulation bound of the oracle and repeats its own bits."""
+    t, k, n = 16, 2048, 200
+    x = normal(t * k, 41, ks).reshape(t, k)
+    w = _bf16_bits(normal(n * k, 42, ks).reshape(n, k))
+    dx = hip.tensor(x.shape).upload(x)
+    dw = hip.tensor(w.shape, np.uint16).upload(w)
+    hip.set_option("matmul_k_split", ks)
+    try:
+        a = hip.matmul_bf16(dx, dw).numpy()
+        b = hip.matmul_bf16(dx, dw).numpy()
+    finally:
+        hip.set_option("matmul_k_split", 0)
+        dx.free()
+        dw.free()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    want = matmul_bf16(x, w)
+    wf = (w.astype(np.uint32) << 16).view(np.float32)
+    bound = 2 * k * 2.0 ** -24 * (np.abs(x).astype(np.float64) @ np.abs(wf).astype(np.float64).T)
+    assert np.all(np.abs(a.astype(np.float64) - want) <= bound), np.abs(a - want).max()

@@ -77,6 +77,9 @@ struct SubRef {
 static constexpr float kLog2e = 1.4426950408889634f;
 static constexpr int kD = 128;
 static constexpr uint32_t kMaxChunks = 256;
+// Arrival counters (split-K hand-offs) sit one per 128-byte line, in uint32 units:
+// atomics to one line queue behind each other at its L2 channel.
+static constexpr uint32_t kCounterStride = 32;
 
 // Lane l reads lane l^8 (DPP row rotate by 8 within each row of 16 lanes).
 __device__ __forceinline__ float xor8(float x) {
@@ -368,7 +371,7 @@ __device__ __forceinline__ void finish_item(const AttnItem& it, uint32_t kh, uin
       const uint32_t nm = it.pref_nch;
       if (threadIdx.x < nm) {
         const SubRef& sr = members[it.pref_base + threadIdx.x];
-        uint32_t* cnt = counters + static_cast<size_t>(sr.counter) * hkv + kh;
+        uint32_t* cnt = counters + (static_cast<size_t>(sr.counter) * hkv + kh) * kCounterStride;
         const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const bool fin = arrived == sr.nch + it.nch - 1;
         if (fin) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -385,7 +388,7 @@ __device__ __forceinline__ void finish_item(const AttnItem& it, uint32_t kh, uin
     }
   }
   if (threadIdx.x == 0) {
-    uint32_t* cnt = counters + static_cast<size_t>(it.counter) * hkv + kh;
+    uint32_t* cnt = counters + (static_cast<size_t>(it.counter) * hkv + kh) * kCounterStride;
     const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = arrived == total - 1;
     if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -702,7 +702,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   __shared__ uint32_t last_chunk;
   __syncthreads();
   if (threadIdx.x == 0) {
-    uint32_t* cnt = counters + static_cast<size_t>(it.counter) * hkv + kh;
+    uint32_t* cnt = counters + (static_cast<size_t>(it.counter) * hkv + kh) * kCounterStride;
     const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last_chunk = arrived == nch - 1;
     if (last_chunk) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

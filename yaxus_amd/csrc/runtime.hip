@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256) void kv_copy_pages_list(CopyList list,
 // zero by every completed call), then the work list, the shared-prefix member list, the
 // partial maxima/sums and the partial outputs, each 256-byte aligned.
 constexpr size_t kScratchBytes = size_t{16} << 20;
-constexpr size_t kScratchCounterBytes = size_t{64} << 10;
+constexpr size_t kScratchCounterBytes = size_t{1} << 20;
 __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
@@ -326,6 +326,8 @@ struct yx_ctx {
   long decode_shape = 0;
   long cascade = 1;  // attend keys shared by consecutive groups (same pages) once for all of them
   long prefill_split = 1;  // split long prefill tiles along keys when the pass underfills the GPU
+  long matmul_k_split = 0;  // workgroups per matmul output tile along k (0: automatic)
+  long argmax_slices = 0;   // workgroups per argmax row (0: automatic)
   bool profiling = false;
   Profile prof[4];
   bool capturing = false;
@@ -880,7 +882,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
                     : plan->wide    ? static_cast<size_t>((plan->nt + 1) / 2) * 16
                                     : static_cast<size_t>(plan->nt) * 8;
   const size_t po_need = plan->slots * hkv * rps * 128 * 4, pml_need = plan->slots * hkv * rps * 8;
-  const size_t cnt_need = plan->counters * hkv * 4;
+  const size_t cnt_need = plan->counters * hkv * 4 * yx::kCounterStride;
   const void* d_items;
   const yx::SubRef* d_members = nullptr;
   float* po;
@@ -1182,10 +1184,11 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
   if (!c || !key) return fail(YX_ERR_INVALID, "null argument");
   if (value < 0 || (value == 0 && std::strcmp(key, "attn_target_waves") &&
                     std::strcmp(key, "attn_decode_shape") && std::strcmp(key, "attn_cascade") &&
-                    std::strcmp(key, "prefill_split") && std::strcmp(key, "prefill_min_rows")))
+                    std::strcmp(key, "prefill_split") && std::strcmp(key, "prefill_min_rows") &&
+                    std::strcmp(key, "matmul_k_split") && std::strcmp(key, "argmax_slices")))
     return fail(YX_ERR_INVALID,
-                "option values are positive (attn_target_waves, attn_decode_shape, prefill_min_rows: "
-                "0 = automatic; attn_cascade, prefill_split: 0 = off)");
+                "option values are positive (attn_target_waves, attn_decode_shape, prefill_min_rows, "
+                "matmul_k_split, argmax_slices: 0 = automatic; attn_cascade, prefill_split: 0 = off)");
   if (!std::strcmp(key, "attn_target_waves"))
     c->target_waves = value;
   else if (!std::strcmp(key, "attn_max_tiles"))
@@ -1200,6 +1203,10 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
     c->cascade = value ? 1 : 0;
   else if (!std::strcmp(key, "prefill_split"))
     c->prefill_split = value ? 1 : 0;
+  else if (!std::strcmp(key, "matmul_k_split"))
+    c->matmul_k_split = std::min<long>(value, 64);
+  else if (!std::strcmp(key, "argmax_slices"))
+    c->argmax_slices = std::min<long>(value, 1024);
   else
     return fail(YX_ERR_INVALID, std::string("unknown option ") + key);
   ++c->epoch;
@@ -1767,14 +1774,15 @@ int yx_matmul_bf16_dev(yx_ctx* c, const float* x, const uint16_t* w, float* out,
   // Workgroups per output tile along k: about two workgroups per CU in all, each wave
   // at least one pass of its loop (kMmSteps steps of 32).
   const size_t tiles = ((n + 15) / 16) * ((t + 15) / 16), steps = (k + 31) / 32;
-  const size_t ks = std::max<size_t>(1, std::min<size_t>({(2 * static_cast<size_t>(c->cus) + tiles - 1) / tiles,
-                                                           steps / (yx::kMmWaves * yx::kMmSteps), 64}));
+  size_t ks = std::max<size_t>(1, std::min<size_t>({(2 * static_cast<size_t>(c->cus) + tiles - 1) / tiles,
+                                                     steps / (yx::kMmWaves * yx::kMmSteps), 64}));
+  if (c->matmul_k_split > 0) ks = std::min<size_t>(static_cast<size_t>(c->matmul_k_split), steps);
   if (ks > 1) {
-    if (c->capturing && (c->mm_part.cap < tiles * ks * 1024 || c->mm_counters.cap < tiles * 4))
+    if (c->capturing && (c->mm_part.cap < tiles * ks * 1024 || c->mm_counters.cap < tiles * 4 * yx::kCounterStride))
       return fail(YX_ERR_INVALID, "run the call once before capturing it (its scratch is allocated then)");
     if (tiles * ks * 1024 > 0xffffffffu) return fail(YX_ERR_UNSUPPORTED, "matmul dimensions too large");
     if ((rc = c->mm_part.ensure(tiles * ks * 1024, c->stream))) return rc;
-    if ((rc = c->mm_counters.ensure(tiles * 4, c->stream, true))) return rc;
+    if ((rc = c->mm_counters.ensure(tiles * 4 * yx::kCounterStride, c->stream, true))) return rc;
   }
   hipLaunchKernelGGL(yx::matmul_bf16_rows,
                      dim3(static_cast<unsigned>((n + 15) / 16), static_cast<unsigned>((t + 15) / 16),
@@ -1798,11 +1806,12 @@ int yx_argmax_rows_dev(yx_ctx* c, const float* logits, size_t rows, size_t cols,
   // Slices per row: each thread's share of a slice in one pass of its loads
   // (kArgmaxQuads quads), so a slice takes one round trip to memory.
   const size_t per_slice = static_cast<size_t>(yx::kArgmaxThreads) * yx::kArgmaxQuads * 4;
-  const size_t nsl = std::max<size_t>(1, std::min<size_t>((cols + per_slice - 1) / per_slice, 1024));
-  if (c->capturing && (c->am_keys.cap < rows * nsl * 8 || c->am_counters.cap < rows * 4))
+  size_t nsl = std::max<size_t>(1, std::min<size_t>((cols + per_slice - 1) / per_slice, 1024));
+  if (c->argmax_slices > 0) nsl = std::min<size_t>(static_cast<size_t>(c->argmax_slices), cols);
+  if (c->capturing && (c->am_keys.cap < rows * nsl * 8 || c->am_counters.cap < rows * 4 * yx::kCounterStride))
     return fail(YX_ERR_INVALID, "run the call once before capturing it (its scratch is allocated then)");
   if ((rc = c->am_keys.ensure(rows * nsl * 8, c->stream))) return rc;
-  if ((rc = c->am_counters.ensure(rows * 4, c->stream, true))) return rc;
+  if ((rc = c->am_counters.ensure(rows * 4 * yx::kCounterStride, c->stream, true))) return rc;
   hipLaunchKernelGGL(yx::argmax_rows, dim3(static_cast<unsigned>(nsl), static_cast<unsigned>(rows)),
                      dim3(yx::kArgmaxThreads), 0, c->stream, logits, static_cast<uint32_t>(cols), out,
                      static_cast<unsigned long long*>(c->am_keys.p), static_cast<uint32_t*>(c->am_counters.p));

@@ -111,10 +111,11 @@ __global__ __launch_bounds__(64 * kMmWaves) void matmul_bf16_rows(const float* _
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-      const uint32_t arrived = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED,
+      uint32_t* cnt = counters + tile * kCounterStride;
+      const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED,
                                                       __HIP_MEMORY_SCOPE_AGENT);
       last = arrived == ks - 1;
-      if (last) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!last || wave != 0) return;
@@ -215,10 +216,11 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_rows(const float* __res
       __hip_atomic_store(keys + static_cast<size_t>(row) * nsl + slice, b, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
       __builtin_amdgcn_s_waitcnt(0);
-      const uint32_t arrived = __hip_atomic_fetch_add(counters + row, 1u, __ATOMIC_RELAXED,
+      uint32_t* cnt = counters + static_cast<size_t>(row) * kCounterStride;
+      const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED,
                                                       __HIP_MEMORY_SCOPE_AGENT);
       last = arrived == nsl - 1;
-      if (last) __hip_atomic_store(counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   __syncthreads();
