@@ -72,12 +72,14 @@ int yx_sync(yx_ctx* ctx);
  * prefill tiles much longer than the average load of a workgroup slot, e.g. a chunk of
  * one long sequence, are split along keys and their partial results merged; 0: every
  * tile is one work item). "matmul_k_split" (workgroups per yx_matmul_bf16_dev output
- * tile along k, at most 64; 0, the default: automatic) and "argmax_slices" (workgroups
- * per yx_argmax_rows_dev row, at most 1024; 0, the default: automatic); neither changes
- * argmax's result, and matmul's only by the order of its f32 additions. Setting an
+ * tile along k, at most 64; 0, the default: automatic; it changes the result only by
+ * the order of the f32 additions), "argmax_slices" (workgroups per yx_argmax_rows_dev
+ * row, at most 1024; 0, the default: automatic; the result does not change) and
+ * "prefill_f32_waves" (the f32 arena's prefill tiles: 8 waves of 16 logical rows or 4;
+ * 0, the default: 4 when every sequence of the pass has at most 64 logical rows). Setting an
  * option drops cached work lists. Values are positive; 0 is accepted for
  * attn_target_waves, attn_decode_shape, attn_cascade, prefill_split, prefill_min_rows,
- * matmul_k_split and argmax_slices. */
+ * matmul_k_split, argmax_slices and prefill_f32_waves (which takes 0, 4 or 8). */
 int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
 /* Counters of the context since its creation: "page_entries_sent" (page-table entries
  * yx_pass_begin uploaded), "page_runs_sent" (runs of consecutive entries they formed)
@@ -91,7 +93,8 @@ int yx_ctx_get_stat(yx_ctx* ctx, const char* key, uint64_t* out);
  * pages of `page_size` tokens (a multiple of 16), zeroed. dtype YX_DTYPE_F16 (binary16,
  * the fast path) or YX_DTYPE_F32 (the reference's own K/V precision: stores are exact,
  * attention runs on f32 MFMAs: split-K decode items of at most 16 (row, q head) pairs,
- * or prefill tiles of 128, chosen by the prefill_min_rows option of yx_ctx_set_option;
+ * or prefill tiles of 128 or 64, chosen as the options prefill_min_rows and
+ * prefill_f32_waves of yx_ctx_set_option describe;
  * at most 16 q heads per KV head; write_rows as its own launch). */
 int yx_kv_create(yx_ctx* ctx, size_t layers, size_t pages, size_t page_size, size_t hkv,
                  size_t head_dim, int dtype, yx_kv** out);

@@ -61,13 +61,16 @@ def test_f32_decode_and_verify_match_oracle(hip, hq, hkv, page, window, k):
     sc.kv.destroy()
 
 
-@pytest.fixture(autouse=True)
-def _prefill_from_32_rows(hip):
+@pytest.fixture(autouse=True, params=[8, 4], ids=["tiles128", "tiles64"])
+def _prefill_from_32_rows(hip, request):
     """The prefill kernel for every pass with 32 or more rows of one sequence (the
-    automatic choice would attend these small passes as decode items)."""
+    automatic choice would attend these small passes as decode items), with tiles of
+    128 logical rows (8 waves) and of 64 (4 waves, two workgroups per CU)."""
     hip.set_option("prefill_min_rows", 32)
+    hip.set_option("prefill_f32_waves", request.param)
     yield
     hip.set_option("prefill_min_rows", 0)
+    hip.set_option("prefill_f32_waves", 0)
 
 
 @contextlib.contextmanager

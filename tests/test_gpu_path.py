@@ -264,18 +264,19 @@ def test_prefill_tiles_match_oracle(hip, hq, hkv, page, window, chunk):
 
 
 @pytest.mark.parametrize("hq,hkv,page,window,prior,chunk,f32", [
-    (16, 4, 16, 0, 3000, 64, False), (16, 4, 16, 2000, 3000, 64, False),
-    (8, 2, 32, 0, 5000, 33, False), (32, 2, 16, 0, 2500, 40, False),
-    (16, 4, 64, 0, 4100, 256, False), (16, 4, 16, 0, 4000, 64, True),
-    (8, 2, 32, 1500, 5000, 130, True)])
+    (16, 4, 16, 0, 3000, 64, 0), (16, 4, 16, 2000, 3000, 64, 0),
+    (8, 2, 32, 0, 5000, 33, 0), (32, 2, 16, 0, 2500, 40, 0),
+    (16, 4, 64, 0, 4100, 256, 0), (16, 4, 16, 0, 4000, 64, 8),
+    (8, 2, 32, 1500, 5000, 130, 8), (16, 4, 16, 0, 4000, 64, 4),
+    (8, 2, 32, 1500, 5000, 130, 4)])
 def test_prefill_split_along_keys(hip, hq, hkv, page, window, prior, chunk, f32):
     """One long sequence's chunk: too few tiles to fill the GPU, so each tile's keys are
     split over several work items whose partial softmaxes the tile's last chunk merges.
     Against the oracle (to 2e-5), against the same pass with the split off, and bit for
     bit from call to call (the merge runs in chunk order). A second, short sequence in
     the same pass keeps its tiles whole. Both arenas (binary16, and f32 with its own
-    prefill kernel)."""
-    sc = Scenario(hip, pages=(prior + chunk) // page + 64, page=page, hkv=hkv, pool_seed=7, f32=f32)
+    prefill kernel, in tiles of 128 and of 64 logical rows: f32 = its waves)."""
+    sc = Scenario(hip, pages=(prior + chunk) // page + 64, page=page, hkv=hkv, pool_seed=7, f32=bool(f32))
     a, b = sc.cache.new_seq(), sc.cache.new_seq()
     sc.prefill({a: prior, b: 40})
     pr = sc.run_pass([(a, chunk), (b, 20)])
@@ -284,6 +285,7 @@ def test_prefill_split_along_keys(hip, hq, hkv, page, window, prior, chunk, f32)
     q = sc.draw(rows * hq * D).reshape(rows, hq * D)
     want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages, window=window)
     hip.set_option("prefill_min_rows", 1)  # the prefill kernel (few tiles: decode by default)
+    hip.set_option("prefill_f32_waves", f32)
     try:
         split0 = hip.stat("prefill_split_tiles")
         got = hip.attend(sc.kv, 0, q, hq, window=window)
@@ -296,6 +298,7 @@ def test_prefill_split_along_keys(hip, hq, hkv, page, window, prior, chunk, f32)
             hip.set_option("prefill_split", 1)
     finally:
         hip.set_option("prefill_min_rows", 0)
+        hip.set_option("prefill_f32_waves", 0)
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
     for x in (got, whole):
         err = np.abs(x - want).max()

@@ -29,12 +29,22 @@
 
 namespace yx {
 
+// Two shapes: 8 waves (128 logical rows) with a 4-stage ring, one workgroup per CU; or
+// 4 waves (64 rows) with a 2-stage ring (64 KiB), two workgroups per CU, for passes
+// whose sequences have few rows (a tile of 128 would leave most of its waves idle).
+template <int W>
+struct Pf32Shape {
+  static constexpr int kRows = W * 16;             // logical rows per work item (one tile per wave)
+  static constexpr int kRing = W == 8 ? 4 : 2;     // LDS stages (32 KiB each)
+  static constexpr int kLead = kRing - 1;          // stages in flight ahead of the one computed
+  static constexpr int kRowsPerWave = 32 / W;      // stage rows (1 KiB each) each wave moves
+};
 static constexpr int kPf32Waves = 8;
-static constexpr int kPf32Rows = kPf32Waves * 16;  // logical rows per work item (one tile per wave)
-static constexpr int kPf32Ring = 4;               // LDS stages (32 KiB each)
-static constexpr int kPf32Lead = kPf32Ring - 1;   // stages in flight ahead of the one computed
+static constexpr int kPf32Rows = Pf32Shape<8>::kRows;
+static constexpr int kPf32SmallRows = Pf32Shape<4>::kRows;
 
-__global__ __launch_bounds__(64 * kPf32Waves) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_attn_prefill_f32(
+template <int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void paged_attn_prefill_f32(
     const PrefillItem* __restrict__ items, const uint32_t* pos,
     const uint32_t* __restrict__ pages, const float* __restrict__ kc, const float* __restrict__ vc,
     const float* q, float* __restrict__ out, uint32_t hq, uint32_t hkv, uint32_t bpp_shift,
@@ -43,7 +53,9 @@ __global__ __launch_bounds__(64 * kPf32Waves) __attribute__((amdgpu_waves_per_eu
   // A ring of stages; each is 32 rows of 1 KiB: K of block b as rows 8b + t ([t][g][key c],
   // float4 = K[c][16t + 4g .. + 3]), then V of block b as rows 16 + 8b + 2t + h
   // ([t][h][g][c], float4 = V[4g + t][64h + 4c .. + 3]).
-  __shared__ float4 ring[kPf32Ring][32 * 64];
+  using S = Pf32Shape<W>;
+  constexpr int kRing = S::kRing, kLead = S::kLead, kRpw = S::kRowsPerWave;
+  __shared__ float4 ring[kRing][32 * 64];
   const PrefillItem it = items[blockIdx.x / hkv];
   const uint32_t kh = blockIdx.x % hkv;
   const int tid = threadIdx.x;
@@ -58,13 +70,15 @@ __global__ __launch_bounds__(64 * kPf32Waves) __attribute__((amdgpu_waves_per_eu
   const uint32_t nblk = it.blk1 - it.blk0;
   const uint32_t nst = (nblk + 1) / 2;  // stages of two blocks
 
-  // Wave w moves rows 4w .. 4w + 3 of each stage: all of one block's K (w < 4) or V.
-  const bool my_v = wave >= 4;
-  const uint32_t my_blk = static_cast<uint32_t>((wave & 3) >> 1);
-  uint32_t src_off[4];  // bytes within the block, per row
+  // Wave w moves stage rows kRpw * w .. kRpw * (w + 1) - 1, all of one block's K (rows
+  // 0-15) or V (rows 16-31).
+  const int row0 = wave * kRpw;
+  const bool my_v = row0 >= 16;
+  const uint32_t my_blk = static_cast<uint32_t>((row0 & 15) >> 3);
+  uint32_t src_off[kRpw];  // bytes within the block, per row
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int row = (wave & 1) * 4 + r;  // row within the block's 8 rows
+  for (int r = 0; r < kRpw; ++r) {
+    const int row = (row0 & 7) + r;  // row within the block's 8 rows
     if (!my_v)
       src_off[r] = static_cast<uint32_t>((c * kD + 16 * row + 4 * g) * 4);
     else
@@ -84,10 +98,9 @@ __global__ __launch_bounds__(64 * kPf32Waves) __attribute__((amdgpu_waves_per_eu
                         static_cast<size_t>(next_page.y) * 16 * kD;
     next_page = page_of(st + 1);
     const char* blk = reinterpret_cast<const char*>((my_v ? vc : kc) + elem);
-    const uint32_t dst = ring_base + (st & (kPf32Ring - 1)) * (32 * 1024) +
-                         (my_v ? 16u * 1024u : 0u) + my_blk * 8192u + (wave & 1) * 4096u;
+    const uint32_t dst = ring_base + (st & (kRing - 1)) * (32 * 1024) + static_cast<uint32_t>(row0) * 1024u;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) load_to_lds16(blk + src_off[r], dst + r * 1024);
+    for (int r = 0; r < kRpw; ++r) load_to_lds16(blk + src_off[r], dst + r * 1024);
   };
 
   // This lane's column: its row position, key window and q (dims 16t + 4g + 0..3) as
@@ -108,7 +121,7 @@ __global__ __launch_bounds__(64 * kPf32Waves) __attribute__((amdgpu_waves_per_eu
   __asm__ volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int j = 0; j < kPf32Lead; ++j) issue(j);
+  for (int j = 0; j < kLead; ++j) issue(j);
 #pragma unroll
   for (int t = 0; t < 8; ++t)
     if (!has) qv[t] = float4{0, 0, 0, 0};
@@ -191,14 +204,14 @@ __global__ __launch_bounds__(64 * kPf32Waves) __attribute__((amdgpu_waves_per_eu
   };
 
   for (uint32_t st = 0; st < nst; ++st) {
-    // This wave's loads of stage st are done when at most the kPf32Lead - 1 later
-    // stages' are in flight; the barrier makes every wave's rows visible, and every wave
-    // has finished computing stage st - 1, whose slot stage st + kPf32Lead refills.
-    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (kPf32Lead - 1)) : "memory");
+    // This wave's loads of stage st are done when at most the kLead - 1 later stages'
+    // are in flight; the barrier makes every wave's rows visible, and every wave has
+    // finished computing stage st - 1, whose slot stage st + kLead refills.
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(kRpw * (kLead - 1)) : "memory");
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
-    issue(st + kPf32Lead);
-    const float4* sb = &ring[st & (kPf32Ring - 1)][0];
+    issue(st + kLead);
+    const float4* sb = &ring[st & (kRing - 1)][0];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int key0 = first_key + static_cast<int>(st * 32 + b * 16);
@@ -233,7 +246,7 @@ __global__ __launch_bounds__(64 * kPf32Waves) __attribute__((amdgpu_waves_per_eu
   const __amdgpu_buffer_rsrc_t rml = make_rsrc(part_ml, part_ml_bytes);
   if (has) {
     const size_t slot = (static_cast<size_t>(it.part_base) + (it.chunk_nch & 0xffffu)) * hkv + kh;
-    const size_t e = slot * kPf32Rows + lr;
+    const size_t e = slot * S::kRows + lr;
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
@@ -253,7 +266,7 @@ __global__ __launch_bounds__(64 * kPf32Waves) __attribute__((amdgpu_waves_per_eu
   }
   __syncthreads();
   if (!last_chunk) return;
-  merge_tile<64 * kPf32Waves, kPf32Rows>(it.r0, it.nrows, it.part_base, nch, kh, G, hq, hkv, out, ro, rml);
+  merge_tile<64 * W, S::kRows>(it.r0, it.nrows, it.part_base, nch, kh, G, hq, hkv, out, ro, rml);
 }
 
 }  // namespace yx

@@ -171,6 +171,7 @@ struct AttnPlan {
   bool small_units = false;  // balanced with items of at most 2 * kBalQuads blocks: 2-block units
   bool wide = false;  // 16-row tiles (the wide kernel) instead of 8-row ones
   bool f32 = false;   // the f32-arena kernel
+  int pf32_waves = 8;  // f32 prefill tiles: 8 waves (128 logical rows) or 4 (64)
   std::vector<yx::AttnItem> items;
   DevBuf d_items;
   std::vector<yx::SubRef> members;  // member groups of shared prefixes
@@ -328,6 +329,7 @@ struct yx_ctx {
   long prefill_split = 1;  // split long prefill tiles along keys when the pass underfills the GPU
   long matmul_k_split = 0;  // workgroups per matmul output tile along k (0: automatic)
   long argmax_slices = 0;   // workgroups per argmax row (0: automatic)
+  long pf32_waves = 0;      // f32 prefill tile shape: 4 or 8 waves (0: automatic)
   bool profiling = false;
   Profile prof[4];
   bool capturing = false;
@@ -482,7 +484,12 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
     AttnPlan plan;
     plan.prefill = true;
     plan.f32 = f32;
-    const size_t tile_rows = f32 ? yx::kPf32Rows : yx::kPrefillRows;
+    // f32 tiles of 64 logical rows (two 4-wave workgroups per CU) when every sequence's
+    // rows fit one (option prefill_f32_waves: 4 or 8 fixes the shape).
+    if (f32)
+      plan.pf32_waves = c->pf32_waves ? static_cast<int>(c->pf32_waves)
+                                      : (max_rows * G <= static_cast<size_t>(yx::kPf32SmallRows) ? 4 : 8);
+    const size_t tile_rows = !f32 ? yx::kPrefillRows : plan.pf32_waves == 4 ? yx::kPf32SmallRows : yx::kPf32Rows;
     const uint32_t per = static_cast<uint32_t>(std::max<size_t>(1, tile_rows / G));
     if (G > tile_rows)
       return fail(YX_ERR_UNSUPPORTED, "more query heads per KV head than a prefill tile holds");
@@ -514,8 +521,8 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
       uint64_t total = 0;
       for (const yx::PrefillItem& w : plan.pitems) total += (w.blk1 - w.blk0 + 1) / 2 + kFixedPairs;
       total *= hkv;
-      // Workgroup slots: two per CU (4-wave binary16 tiles), one (8-wave f32 tiles).
-      const uint64_t slots2 = (f32 ? 1 : 2) * static_cast<uint64_t>(c->cus);
+      // Workgroup slots: two per CU (4-wave tiles), one (8-wave f32 tiles).
+      const uint64_t slots2 = (f32 && plan.pf32_waves == 8 ? 1 : 2) * static_cast<uint64_t>(c->cus);
       const uint64_t avg = std::max<uint64_t>(kMinChunkPairs, (total + slots2 - 1) / slots2);
       std::vector<yx::PrefillItem> split;
       uint32_t nslot = 0, ncnt = 0;
@@ -883,7 +890,9 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
       c->used_keys.push_back(key);
   }
   // Logical rows per partial slot: the kernel's tile rows.
-  const size_t rps = plan->prefill ? static_cast<size_t>(plan->f32 ? yx::kPf32Rows : yx::kPrefillRows)
+  const size_t rps = plan->prefill ? static_cast<size_t>(!plan->f32 ? yx::kPrefillRows
+                                                       : plan->pf32_waves == 4 ? yx::kPf32SmallRows
+                                                                               : yx::kPf32Rows)
                     : plan->wide    ? static_cast<size_t>((plan->nt + 1) / 2) * 16
                                     : static_cast<size_t>(plan->nt) * 8;
   const size_t po_need = plan->slots * hkv * rps * 128 * 4, pml_need = plan->slots * hkv * rps * 8;
@@ -955,8 +964,9 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
     if (po_cap > 0xffffffffu || pml_cap > 0xffffffffu)
       return fail(YX_ERR_UNSUPPORTED, "prefill partials beyond 4 GiB");
     const uint32_t pf_po_bytes = static_cast<uint32_t>(po_cap), pf_pml_bytes = static_cast<uint32_t>(pml_cap);
-    if (plan->f32)
-      hipLaunchKernelGGL(yx::paged_attn_prefill_f32, pgrid, dim3(64 * yx::kPf32Waves), 0, c->stream,
+    if (plan->f32) {
+      auto* kern = plan->pf32_waves == 4 ? yx::paged_attn_prefill_f32<4> : yx::paged_attn_prefill_f32<8>;
+      hipLaunchKernelGGL(kern, pgrid, dim3(64 * plan->pf32_waves), 0, c->stream,
                          static_cast<const yx::PrefillItem*>(d_items), c->dev_pos,
                          static_cast<const uint32_t*>(c->d_pages.p),
                          reinterpret_cast<const float*>(kv->k[layer]),
@@ -964,7 +974,7 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
                          static_cast<uint32_t>(hq), static_cast<uint32_t>(hkv), shift,
                          static_cast<uint32_t>(window), scale * yx::kLog2e, po, pml, cnt,
                          pf_po_bytes, pf_pml_bytes);
-    else if (qkv)
+    } else if (qkv)
       hipLaunchKernelGGL((yx::paged_attn_prefill<true>), pgrid, dim3(64 * yx::kPrefillWaves), 0, c->stream,
                        static_cast<const yx::PrefillItem*>(d_items),
                        c->dev_pos, static_cast<const uint32_t*>(c->d_pages.p),
@@ -1190,7 +1200,8 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
   if (value < 0 || (value == 0 && std::strcmp(key, "attn_target_waves") &&
                     std::strcmp(key, "attn_decode_shape") && std::strcmp(key, "attn_cascade") &&
                     std::strcmp(key, "prefill_split") && std::strcmp(key, "prefill_min_rows") &&
-                    std::strcmp(key, "matmul_k_split") && std::strcmp(key, "argmax_slices")))
+                    std::strcmp(key, "matmul_k_split") && std::strcmp(key, "argmax_slices") &&
+                    std::strcmp(key, "prefill_f32_waves")))
     return fail(YX_ERR_INVALID,
                 "option values are positive (attn_target_waves, attn_decode_shape, prefill_min_rows, "
                 "matmul_k_split, argmax_slices: 0 = automatic; attn_cascade, prefill_split: 0 = off)");
@@ -1210,7 +1221,10 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
     c->prefill_split = value ? 1 : 0;
   else if (!std::strcmp(key, "matmul_k_split"))
     c->matmul_k_split = std::min<long>(value, 64);
-  else if (!std::strcmp(key, "argmax_slices"))
+  else if (!std::strcmp(key, "prefill_f32_waves")) {
+    if (value != 0 && value != 4 && value != 8) return fail(YX_ERR_INVALID, "prefill_f32_waves is 0, 4 or 8");
+    c->pf32_waves = value;
+  } else if (!std::strcmp(key, "argmax_slices"))
     c->argmax_slices = std::min<long>(value, 1024);
   else
     return fail(YX_ERR_INVALID, std::string("unknown option ") + key);
