@@ -446,7 +446,7 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
   } else if (f32) {
     // The f32 arena: its decode items hold 16 logical rows each and re-read their
     // sequence's keys once per item (about 6 TB/s over those reads); its prefill tiles
-    // (128 logical rows, one workgroup per CU) take about 95 us plus 2.4 us per 1024 keys
+    // (64 or 128 logical rows, 8 waves per CU) take about 95 us plus 2.4 us per 1024 keys
     // of the longest context (the key split's chain), or 40 us plus their products at
     // 110 TFLOP/s, whichever is more. The kernel with the smaller estimate runs. Measured
     // (B x rows after ctx, decode / prefill us; the choice was right in 19 of 21 shapes,
