@@ -117,6 +117,29 @@ def test_split_count_does_not_change_results(hip, target_waves, shape):
     assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
 
 
+@pytest.mark.parametrize("lens", [[511], [511] * 4, [1023, 1023], [255] * 8, [40, 500, 7, 300]])
+def test_tiny_passes_split_finely(hip, lens):
+    """Tiny decode passes (at most two 16-key blocks per CU) take one-quad work items,
+    up to 8 chunks per group: against the oracle, bit for bit from call to call, and
+    within tolerance of the same pass split at the coarser default of larger passes."""
+    hq, hkv = 16, 4
+    sc = Scenario(hip, pages=sum(lens) // 16 + 16 * len(lens), page=16, hkv=hkv, pool_seed=13)
+    seqs = [sc.cache.new_seq() for _ in lens]
+    sc.prefill(dict(zip(seqs, lens)))
+    pr = sc.run_pass([(s, 1) for s in seqs])
+    sc.store(pr)
+    q = sc.draw(len(lens) * hq * D).reshape(len(lens), hq * D)
+    got = hip.attend(sc.kv, 0, q, hq)
+    again = hip.attend(sc.kv, 0, q, hq)
+    with option(hip, "attn_target_waves", 64):  # one item per group or few chunks
+        coarse = hip.attend(sc.kv, 0, q, hq)
+    want = sc.orc[0].attend(q, hq, pr.meta.pos, pr.meta.pt_off, pr.meta.pages)
+    assert close(got, want).all(), f"max abs err {np.abs(got - want).max()}"
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    assert np.abs(got - coarse).max() < 2e-5
+    sc.kv.destroy()
+
+
 @pytest.mark.parametrize("shape", [0, 1])
 @pytest.mark.parametrize("hq,hkv,k", [(16, 4, 6), (16, 4, 5), (16, 4, 7), (8, 8, 3), (16, 1, 2),
                                       (32, 1, 1), (12, 4, 4)])
