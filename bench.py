@@ -63,14 +63,54 @@ def build_pass(KvCache):
     return cache, pr
 
 
+BOX_CPU_SHARE = 16  # host threads one GPU's job may keep busy on the GPU boxes
+
+
+def cpu_threads():
+    """The reference CPU backend's pool size (crates/yaxus-backend-cpu/src/threads.rs:4-31):
+    physical cores, SMT siblings counted once (distinct
+    /sys/devices/system/cpu/cpuN/topology/thread_siblings_list), capped by the available
+    parallelism (the affinity mask and a cgroup CPU quota, as Rust's
+    std::thread::available_parallelism counts them); here also capped by the GPU box's
+    CPU share for one GPU."""
+    logical = len(os.sched_getaffinity(0))
+    avail = logical
+    try:  # cgroup v2 quota: "max 100000" or "<quota> <period>"
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            avail = max(1, min(avail, -(-int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    sib = set()
+    base = "/sys/devices/system/cpu"
+    try:
+        for name in os.listdir(base):
+            if name.startswith("cpu") and name[3:].isdigit():
+                try:
+                    with open(os.path.join(base, name, "topology", "thread_siblings_list")) as f:
+                        sib.add(f.read().strip())
+                except OSError:
+                    pass
+    except OSError:
+        pass
+    physical = len(sib) or None
+    n = min(physical, avail) if physical else avail
+    threads = min(n, BOX_CPU_SHARE)
+    return {"physical_cores": physical, "logical_cpus": logical, "available_parallelism": avail,
+            "threads": threads,
+            "rule": "min(physical cores, available parallelism) as threads.rs:4-31, "
+                    f"capped at the box's {BOX_CPU_SHARE}-thread share"}
+
+
 def cpu_baseline(pr, budget_s=10.0):
     """The oracle's restatement of CpuBackend::attend (f16 KV, f32 math), threaded like
     the reference's rayon pool, on one layer-step of the same workload."""
     from oracle.attn import OracleArena, lib
 
     lib()
-    threads = len(os.sched_getaffinity(0))
-    threads = min(threads, 16)
+    cpu = cpu_threads()
+    threads = cpu["threads"]
     arena = OracleArena(POOL, PAGE, HKV, D, f16=True)
     rng = np.random.default_rng(SEED)
     arena.k[:] = rng.standard_normal(arena.k.shape, dtype=np.float32).astype(np.float16).view(np.uint16)
@@ -90,7 +130,11 @@ def cpu_baseline(pr, budget_s=10.0):
         "unit": "GB/s",
         "us_per_layer_step": round(us, 1),
         "cores": threads,
-        "host_cpus": len(os.sched_getaffinity(0)),
+        "physical_cores": cpu["physical_cores"],
+        "logical_cpus": cpu["logical_cpus"],
+        "available_parallelism": cpu["available_parallelism"],
+        "threads": threads,
+        "thread_rule": cpu["rule"],
         "kind": "port",
         "sample": f"{reps} layer-steps of B=16 ctx 4096 (1 layer, attend only) in {el:.1f} s",
     }
@@ -651,6 +695,8 @@ def main():
             "avg_launch_us_isolated": round(isolated_us, 3),
             "bytes_per_launch": ATTN_BYTES,
             "traffic": traffic_from_profiles(),
+            "traffic_source": "profiles/attn_decode_b16_ctx4096_traffic.json (rocprofv3 --pmc "
+                              "FETCH_SIZE and WRITE_SIZE runs of bench.py --profile-run, committed)",
         },
         "cpu_baseline": None if (args.no_cpu or args.profile_run) else cpu_baseline(pr, args.cpu_seconds),
     }

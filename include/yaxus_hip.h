@@ -176,14 +176,19 @@ int yx_attention_append_dev(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k
 
 /* No counterpart in the reference: yx_attention_append_dev for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). Same kernels, arguments and results; the split-K work list, partials and
- * arrival counters live in the library's static device scratch (16 MiB per GPU, of
- * which 1 MiB holds 8192 counters, one per 128-byte line; held
- * until the process ends) instead of buffers of the context, so the call makes no
- * device or pinned-host allocation (the pass's pinned staging from yx_pass_begin must
- * hold the work list). A pass whose work list and partials do not fit the scratch is
- * refused with YX_ERR_UNSUPPORTED. Every call on a GPU shares that GPU's scratch:
- * calls that overlap on one GPU (other streams or contexts) race. */
+ * hipMalloc). Same kernels, arguments and results; the split-K partials and arrival
+ * counters live in the library's static device scratch (16 MiB per GPU: 1 MiB of
+ * counters, 8192 of them, one per 128-byte line; a 2 MiB region for work lists; the
+ * rest for partials; held until the process ends) instead of buffers of the context,
+ * so the call makes no device or pinned-host allocation. The work list is the one
+ * yx_pass_begin put on the device when the previous pass made the same call (a decode
+ * loop's steady state), else it is sent once per pass into the scratch's list region
+ * from the pass's pinned staging. A pass whose work lists or partials do not fit is
+ * refused with YX_ERR_UNSUPPORTED. Every call on a GPU shares that GPU's scratch: when a
+ * call comes from another context than the last one, its stream first waits for the
+ * other context's stream (an event, no allocation), so contexts take turns; under graph
+ * capture such a hand-over cannot be recorded and is refused (make one eager call
+ * first). Calls that overlap in any other way race. */
 int yx_attention_append_noalloc(yx_ctx* ctx, yx_kv* kv, size_t layer, const float* k,
                                 const float* v, const float* q, float* out, size_t hq,
                                 size_t hkv, size_t window, float scale);

@@ -2,6 +2,8 @@
 
 - ``yaxus_amd/libyaxus_kv.so``  host page allocator (g++), C ABI of include/yaxus_kv_cache.h
 - ``yaxus_amd/libyaxus_hip.so`` device path for gfx950 (hipcc), C ABI of include/yaxus_hip.h
+- ``tests/native/*``            C++ programs over the C ABIs, one of them (``kv_replay_asan``)
+  with the allocator built under ASan + UBSan
 
 ``python -m yaxus_amd.build`` compiles both; it always recompiles.
 """
@@ -62,6 +64,20 @@ def build_native_tests():
           "-L" + HERE, "-lyaxus_kv", "-Wl,-rpath,$ORIGIN/../../yaxus_amd", "-o", NATIVE_FORK])
 
 
+NATIVE_REPLAY_ASAN = os.path.join(ROOT, "tests", "native", "kv_replay_asan")
+
+
+def build_sanitized():
+    """The allocator (kv_cache.cpp) compiled into the replay program of tests/native under
+    AddressSanitizer and UndefinedBehaviorSanitizer, for the CPU tests: every out-of-bounds
+    index, use after free, leak or undefined operation in its page-vector arithmetic
+    aborts the run (halt_on_error)."""
+    _run(["g++", "-O1", "-g", "-std=c++17", "-Wall", "-Wextra",
+          "-fsanitize=address,undefined", "-fno-sanitize-recover=all", "-fno-omit-frame-pointer",
+          NATIVE_REPLAY_ASAN.replace("_asan", "") + ".cpp", os.path.join(CSRC, "kv_cache.cpp"),
+          "-o", NATIVE_REPLAY_ASAN])
+
+
 def build_oracle():
     _run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "-B"])
 
@@ -70,6 +86,7 @@ def build_all():
     build_kv()
     build_hip()
     build_native_tests()
+    build_sanitized()
     build_oracle()
 
 

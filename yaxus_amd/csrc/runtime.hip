@@ -216,15 +216,32 @@ __global__ __launch_bounds__(256) void kv_copy_pages_list(CopyList list,
 // ends. Its device address is taken once per device (hipGetSymbolAddress, at the first
 // context on the device) and used everywhere host code needs the memory: the array's
 // name is only a host-side stand-in. Layout: arrival counters (zeroed at set-up, left at
-// zero by every completed call), then the work list, the shared-prefix member list, the
-// partial maxima/sums and the partial outputs, each 256-byte aligned.
+// zero by every completed call), a region for work lists, then the partial maxima/sums
+// and the partial outputs, each 256-byte aligned.
 constexpr size_t kScratchBytes = size_t{16} << 20;
 constexpr size_t kScratchCounterBytes = size_t{1} << 20;
+constexpr size_t kScratchListBytes = size_t{2} << 20;
 __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+
+// Who used a device's scratch last, and which work lists its list region holds. A
+// context's lists stay valid for the pass (epoch) they were built for; a call from
+// another context first makes its stream wait for the previous user's stream (an event
+// recorded there at the hand-over), so calls on different streams do not overlap on
+// the scratch.
+using PlanKey = std::tuple<size_t, size_t, size_t, bool, size_t>;  // (window, hq, hkv, f32, page)
+struct ScratchOwner {
+  const yx_ctx* ctx = nullptr;
+  hipStream_t stream = nullptr;
+  uint64_t epoch = 0;
+  size_t list_used = 0;
+  std::vector<std::pair<PlanKey, std::pair<size_t, size_t>>> lists;  // key -> (items, members) offsets
+  hipEvent_t handover = nullptr;
+};
+ScratchOwner g_scratch_owner[kMaxDevices];
 
 __global__ void zero_u32(uint32_t* p, uint32_t n) {
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
@@ -242,8 +259,22 @@ int scratch_init(int device, hipStream_t s) {
                      static_cast<uint32_t>(kScratchCounterBytes / 4));
   YX_HIP(hipGetLastError());
   YX_HIP(hipStreamSynchronize(s));
+  YX_HIP(hipEventCreateWithFlags(&g_scratch_owner[device].handover, hipEventDisableTiming));
   g_scratch_ptr[device] = ptr;
   return YX_OK;
+}
+
+// A context that goes away stops being the scratch's owner (its stream is destroyed).
+void scratch_forget(const yx_ctx* c, int device) {
+  if (device < 0 || device >= kMaxDevices) return;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchOwner& o = g_scratch_owner[device];
+  if (o.ctx == c) {
+    o.ctx = nullptr;
+    o.stream = nullptr;
+    o.lists.clear();
+    o.list_used = 0;
+  }
 }
 
 struct ScratchMap {
@@ -357,27 +388,84 @@ struct yx_ctx {
 namespace {
 
 // Regions of the device's scratch for one no-alloc call; refuses sizes beyond it.
-int scratch_map(yx_ctx* c, size_t items, size_t members, size_t part_ml, size_t part_o,
-                size_t counters, ScratchMap* m) {
+int scratch_map(yx_ctx* c, size_t part_ml, size_t part_o, size_t counters, ScratchMap* m) {
   char* base = static_cast<char*>(g_scratch_ptr[c->device]);
   if (!base) return fail(YX_ERR_INVALID, "scratch not set up on this device");
   if (counters > kScratchCounterBytes)
     return fail(YX_ERR_UNSUPPORTED, "no-alloc call: the pass needs more arrival counters than the scratch holds");
   auto r256 = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
-  size_t off = kScratchCounterBytes;
+  size_t off = kScratchCounterBytes + kScratchListBytes;
   m->counters = base;
-  m->items = base + off;
-  off += r256(items);
-  m->members = base + off;
-  off += r256(members);
+  m->items = m->members = nullptr;
   m->part_ml = base + off;
   off += r256(part_ml);
   m->part_o = base + off;
   off += r256(part_o);
   if (off > kScratchBytes)
-    return fail(YX_ERR_UNSUPPORTED, "no-alloc call: the pass's work list and split-K partials need " +
+    return fail(YX_ERR_UNSUPPORTED, "no-alloc call: the pass's split-K partials need " +
                                         std::to_string(off) + " bytes, more than the " +
                                         std::to_string(kScratchBytes) + "-byte scratch");
+  return YX_OK;
+}
+
+// Takes the device's scratch for context c: when another context used it last, c's
+// stream first waits for everything issued on that context's stream so far (one event,
+// no allocation). Under graph capture the wait cannot be recorded, so a hand-over there
+// is refused. Then finds the plan's work lists in the scratch's list region, or sends
+// them there from the pass's pinned staging (once per plan and pass); plans whose lists
+// yx_pass_begin already put on the device are read from there instead.
+int scratch_take(yx_ctx* c, const PlanKey& key, AttnPlan* plan, ScratchMap* m) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchOwner& o = g_scratch_owner[c->device];
+  if (o.ctx != c) {
+    if (o.ctx) {
+      if (c->capturing)
+        return fail(YX_ERR_INVALID, "no-alloc call under capture: another context used this GPU's scratch last; "
+                                    "make one eager call first");
+      YX_HIP(hipEventRecord(o.handover, o.stream));
+      YX_HIP(hipStreamWaitEvent(c->stream, o.handover, 0));
+    }
+    o.ctx = c;
+    o.stream = c->stream;
+    o.lists.clear();
+    o.list_used = 0;
+  }
+  if (plan->uploaded) {
+    m->items = const_cast<void*>(plan->dev_items);
+    m->members = const_cast<void*>(plan->dev_members);
+    return YX_OK;
+  }
+  if (o.epoch != c->epoch) {
+    o.epoch = c->epoch;
+    o.lists.clear();
+    o.list_used = 0;
+  }
+  char* base = static_cast<char*>(g_scratch_ptr[c->device]) + kScratchCounterBytes;
+  for (const auto& e : o.lists)
+    if (e.first == key) {
+      m->items = base + e.second.first;
+      m->members = base + e.second.second;
+      return YX_OK;
+    }
+  auto r256 = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
+  const size_t ib = plan->item_bytes(), mb = plan->members.size() * sizeof(yx::SubRef);
+  if (c->capturing)
+    return fail(YX_ERR_INVALID, "run the call once before capturing it (its work list is uploaded then)");
+  if (o.list_used + r256(ib) + r256(mb) > kScratchListBytes)
+    return fail(YX_ERR_UNSUPPORTED, "no-alloc call: the pass's work lists need more than the scratch's " +
+                                        std::to_string(kScratchListBytes) + "-byte list region");
+  Staging& st = c->staging[c->cur_staging];
+  if (!st.fits(r256(ib) + r256(mb)))
+    return fail(YX_ERR_UNSUPPORTED, "work list larger than the pass's staging buffer (no-alloc call)");
+  const size_t oi = o.list_used, om = oi + r256(ib);
+  const void* items = plan->prefill ? static_cast<const void*>(plan->pitems.data()) : plan->items.data();
+  int rc;
+  if ((rc = st.upload(base + oi, items, ib, c->stream))) return rc;
+  if (mb && (rc = st.upload(base + om, plan->members.data(), mb, c->stream))) return rc;
+  o.list_used = om + r256(mb);
+  o.lists.emplace_back(key, std::make_pair(oi, om));
+  m->items = base + oi;
+  m->members = base + om;
   return YX_OK;
 }
 
@@ -905,20 +993,8 @@ int attention_impl(yx_ctx* c, yx_kv* kv, size_t layer, const float* q, float* ou
   size_t po_cap, pml_cap;
   if (noalloc) {
     ScratchMap m;
-    if ((rc = scratch_map(c, plan->item_bytes(), plan->members.size() * sizeof(yx::SubRef), pml_need,
-                          po_need, cnt_need, &m)))
-      return rc;
-    // The lists go into the scratch on every call (another call may have used it since),
-    // from the pass's pinned staging, which must have room: it is not grown here.
-    Staging& st = c->staging[c->cur_staging];
-    const void* items = plan->prefill ? static_cast<const void*>(plan->pitems.data()) : plan->items.data();
-    auto r256 = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
-    if (!st.fits(r256(plan->item_bytes()) + r256(plan->members.size() * sizeof(yx::SubRef))))
-      return fail(YX_ERR_UNSUPPORTED, "work list larger than the pass's staging buffer (no-alloc call)");
-    if ((rc = st.upload(m.items, items, plan->item_bytes(), c->stream))) return rc;
-    if (!plan->members.empty() &&
-        (rc = st.upload(m.members, plan->members.data(), plan->members.size() * sizeof(yx::SubRef), c->stream)))
-      return rc;
+    if ((rc = scratch_map(c, pml_need, po_need, cnt_need, &m))) return rc;
+    if ((rc = scratch_take(c, std::make_tuple(window, hq, hkv, kv->f32, kv->page), plan, &m))) return rc;
     d_items = m.items;
     d_members = plan->members.empty() ? nullptr : static_cast<const yx::SubRef*>(m.members);
     po = static_cast<float*>(m.part_o);
@@ -1163,6 +1239,7 @@ int yx_ctx_destroy(yx_ctx* c) {
   if (!c) return YX_OK;
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
+  scratch_forget(c, c->device);
   for (auto& p : c->prof)
     for (auto& e : p.pending) {
       (void)hipEventDestroy(e.first);
