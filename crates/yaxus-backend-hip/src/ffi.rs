@@ -99,6 +99,8 @@ unsafe extern "C" {
 
     pub fn yx_dev_alloc(ctx: *mut yx_ctx, bytes: usize, out: *mut *mut c_void) -> c_int;
     pub fn yx_dev_free(ctx: *mut yx_ctx, p: *mut c_void) -> c_int;
+    pub fn yx_host_alloc(ctx: *mut yx_ctx, bytes: usize, out: *mut *mut c_void) -> c_int;
+    pub fn yx_host_free(ctx: *mut yx_ctx, p: *mut c_void) -> c_int;
     pub fn yx_memcpy_h2d(ctx: *mut yx_ctx, dst: *mut c_void, src: *const c_void, bytes: usize) -> c_int;
     pub fn yx_memcpy_d2h(ctx: *mut yx_ctx, dst: *mut c_void, src: *const c_void, bytes: usize) -> c_int;
     pub fn yx_dev_copy(ctx: *mut yx_ctx, dst: *mut c_void, src: *const c_void, bytes: usize) -> c_int;

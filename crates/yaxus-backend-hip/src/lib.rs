@@ -71,12 +71,45 @@ impl Drop for DevBuf {
     }
 }
 
+/// Pinned (page-locked) host staging for the per-layer copies of a wrapped host
+/// backend's tensors: DMA speed both ways, where a pageable Vec is staged through a
+/// driver buffer first.
+struct PinnedBuf {
+    ctx: *mut ffi::yx_ctx,
+    ptr: *mut c_void,
+    bytes: usize,
+}
+
+impl PinnedBuf {
+    fn ensure(slot: &mut Option<PinnedBuf>, ctx: *mut ffi::yx_ctx, bytes: usize) -> Result<*mut c_void> {
+        if slot.as_ref().map_or(true, |b| b.bytes < bytes) {
+            *slot = None;
+            let n = bytes.max(1 << 16);
+            let mut p = ptr::null_mut();
+            // SAFETY: ctx is a live context; p receives n bytes of pinned host memory.
+            check(unsafe { ffi::yx_host_alloc(ctx, n, &mut p) })?;
+            *slot = Some(PinnedBuf { ctx, ptr: p, bytes: n });
+        }
+        Ok(slot.as_ref().unwrap().ptr)
+    }
+}
+
+impl Drop for PinnedBuf {
+    fn drop(&mut self) {
+        // SAFETY: ptr came from yx_host_alloc on this context (which waits for the stream).
+        unsafe { ffi::yx_host_free(self.ctx, self.ptr) };
+    }
+}
+
 /// The paged K/V arena of one model on the device, with each layer's RoPE table
 /// (`[max_pos][head_dim / 2]` cos, then sin, as `Rope::cos_sin` fills it).
 pub struct HipKv {
     ctx: *mut ffi::yx_ctx,
     kv: *mut ffi::yx_kv,
+    /// Distinct RoPE tables; layers with equal tables share one.
     ropes: Vec<DevBuf>,
+    /// Per layer, its table's index in `ropes`.
+    rope_of: Vec<usize>,
     max_pos: usize,
 }
 
@@ -100,7 +133,10 @@ pub struct HipBackend<B: HostTensors> {
     rows: usize,
     qkv: Option<DevBuf>,
     out: Option<DevBuf>,
-    /// Device copies of the q/k norm weights, by the weight's address.
+    pin_in: Option<PinnedBuf>,
+    pin_out: Option<PinnedBuf>,
+    /// Device copies of the q/k norm weights, by the weight's address (cleared with every
+    /// new arena: weights live as long as the model that made it).
     norms: HashMap<usize, DevBuf>,
 }
 
@@ -116,7 +152,8 @@ impl<B: HostTensors> HipBackend<B> {
         let mut ctx = ptr::null_mut();
         // SAFETY: ctx receives a new context handle.
         check(unsafe { ffi::yx_ctx_create(device, &mut ctx) })?;
-        Ok(HipBackend { inner, ctx, rows: 0, qkv: None, out: None, norms: HashMap::new() })
+        Ok(HipBackend { inner, ctx, rows: 0, qkv: None, out: None, pin_in: None, pin_out: None,
+                        norms: HashMap::new() })
     }
 
     pub fn inner(&self) -> &B {
@@ -137,6 +174,8 @@ impl<B: HostTensors> Drop for HipBackend<B> {
     fn drop(&mut self) {
         self.qkv = None;
         self.out = None;
+        self.pin_in = None;
+        self.pin_out = None;
         self.norms.clear();
         // SAFETY: every device buffer of the context is freed above (arenas hold their
         // own context pointer and must be dropped first, as Model drops its Kv first).
@@ -174,15 +213,28 @@ impl<B: HostTensors> Backend for HipBackend<B> {
             ffi::yx_kv_create(self.ctx, metas.len(), pages, PAGE, cfg.num_key_value_heads,
                               cfg.head_dim, ffi::YX_DTYPE_F16, &mut kv)
         })?;
-        let mut arena = HipKv { ctx: self.ctx, kv, ropes: Vec::new(), max_pos };
+        let mut arena = HipKv { ctx: self.ctx, kv, ropes: Vec::new(), rope_of: Vec::new(), max_pos };
+        self.norms.clear();
         let half = cfg.head_dim / 2;
+        // Tables already on the device, with their host copies: a layer whose table
+        // equals one of them (bit for bit) shares it (full and sliding layers usually
+        // differ only in the rope base, so a model holds one or two).
+        let mut seen: Vec<Vec<f32>> = Vec::new();
         for m in metas {
             let mut t = vec![0f32; 2 * max_pos * half];
             let (cos, sin) = t.split_at_mut(max_pos * half);
             for p in 0..max_pos {
                 m.rope.cos_sin(p, &mut cos[p * half..(p + 1) * half], &mut sin[p * half..(p + 1) * half]);
             }
-            arena.ropes.push(DevBuf::upload(self.ctx, &t)?);
+            let same = |a: &Vec<f32>| a.iter().zip(&t).all(|(x, y)| x.to_bits() == y.to_bits());
+            match seen.iter().position(same) {
+                Some(i) => arena.rope_of.push(i),
+                None => {
+                    arena.ropes.push(DevBuf::upload(self.ctx, &t)?);
+                    arena.rope_of.push(seen.len());
+                    seen.push(t);
+                }
+            }
         }
         Ok(arena)
     }
@@ -231,17 +283,22 @@ impl<B: HostTensors> Backend for HipBackend<B> {
         let bytes_out = rows * hq * d * 4;
         let dq = DevBuf::ensure(&mut self.qkv, self.ctx, bytes_in).expect("device buffer");
         let dout = DevBuf::ensure(&mut self.out, self.ctx, bytes_out).expect("device buffer");
+        let pin_in = PinnedBuf::ensure(&mut self.pin_in, self.ctx, bytes_in).expect("pinned buffer");
+        let pin_out = PinnedBuf::ensure(&mut self.pin_out, self.ctx, bytes_out).expect("pinned buffer");
         let mut out = vec![0f32; rows * hq * d];
         let scale = 1.0 / (d as f32).sqrt();
-        // SAFETY: device buffers sized above; the host copies are synchronous.
+        let rope = kv.ropes[kv.rope_of[layer.index]].ptr as *const f32;
+        // SAFETY: device and pinned buffers sized above; the device copies are synchronous,
+        // so the pinned buffers are free again when each returns.
         unsafe {
-            check(ffi::yx_memcpy_h2d(self.ctx, dq, host.as_ptr().cast(), bytes_in)).expect("upload");
+            ptr::copy_nonoverlapping(host.as_ptr().cast::<u8>(), pin_in.cast::<u8>(), bytes_in);
+            check(ffi::yx_memcpy_h2d(self.ctx, dq, pin_in, bytes_in)).expect("upload");
             check(ffi::yx_attention_qkv_dev(self.ctx, kv.kv, layer.index, dq as *const f32, qn, kn,
-                                            kv.ropes[layer.index].ptr as *const f32, kv.max_pos,
-                                            cfg.rms_norm_eps, dout as *mut f32, hq, hkv,
-                                            layer.window.unwrap_or(0), scale))
+                                            rope, kv.max_pos, cfg.rms_norm_eps, dout as *mut f32, hq,
+                                            hkv, layer.window.unwrap_or(0), scale))
                 .expect("attention");
-            check(ffi::yx_memcpy_d2h(self.ctx, out.as_mut_ptr().cast(), dout, bytes_out)).expect("download");
+            check(ffi::yx_memcpy_d2h(self.ctx, pin_out, dout, bytes_out)).expect("download");
+            ptr::copy_nonoverlapping(pin_out.cast::<u8>(), out.as_mut_ptr().cast::<u8>(), bytes_out);
         }
         self.inner.tensor_from_host(rows, hq * d, out)
     }

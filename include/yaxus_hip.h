@@ -68,7 +68,9 @@ int yx_sync(yx_ctx* ctx);
  * every decode pass). "attn_cascade" (1, the default: consecutive groups of a one-tile
  * decode pass whose page tables start with the same pages, e.g. forks of one prompt,
  * attend those shared keys once for all their rows and merge that result into each
- * row's own; 0: every group reads its whole context). "prefill_split" (1, the default:
+ * row's own; 0: every group reads its whole context). "attn_xcd_prefix" (1, the default:
+ * the work items reading one chunk of a shared prefix are placed to run on one XCD, so
+ * they share its L2; 0: in list order; results do not change). "prefill_split" (1, the default:
  * prefill tiles much longer than the average load of a workgroup slot, e.g. a chunk of
  * one long sequence, are split along keys and their partial results merged; 0: every
  * tile is one work item). "matmul_k_split" (workgroups per yx_matmul_bf16_dev output
@@ -78,7 +80,7 @@ int yx_sync(yx_ctx* ctx);
  * "prefill_f32_waves" (the f32 arena's prefill tiles: 8 waves of 16 logical rows or 4;
  * 0, the default: 4 when every sequence of the pass has at most 64 logical rows). Setting an
  * option drops cached work lists. Values are positive; 0 is accepted for
- * attn_target_waves, attn_decode_shape, attn_cascade, prefill_split, prefill_min_rows,
+ * attn_target_waves, attn_decode_shape, attn_cascade, attn_xcd_prefix, prefill_split, prefill_min_rows,
  * matmul_k_split, argmax_slices and prefill_f32_waves (which takes 0, 4 or 8). */
 int yx_ctx_set_option(yx_ctx* ctx, const char* key, long value);
 /* Counters of the context since its creation: "page_entries_sent" (page-table entries
@@ -209,6 +211,11 @@ int yx_argmax_rows_dev(yx_ctx* ctx, const float* logits, size_t rows, size_t col
 /* Device memory and copies on the context's stream (h2d/d2h are synchronous). */
 int yx_dev_alloc(yx_ctx* ctx, size_t bytes, void** out);
 int yx_dev_free(yx_ctx* ctx, void* p);
+/* Pinned (page-locked) host memory, for callers whose data crosses PCIe every layer (a
+ * wrapped host backend's qkv and attention output): copies from and to it run at DMA
+ * speed, where pageable memory is staged through a driver buffer first. */
+int yx_host_alloc(yx_ctx* ctx, size_t bytes, void** out);
+int yx_host_free(yx_ctx* ctx, void* p);
 int yx_memcpy_h2d(yx_ctx* ctx, void* dst, const void* src, size_t bytes);
 int yx_memcpy_d2h(yx_ctx* ctx, void* dst, const void* src, size_t bytes);
 /* Plain device copy kernel (also the reference point for HBM byte counters). */

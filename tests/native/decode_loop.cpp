@@ -4,13 +4,19 @@
 // native engine would run it (crates/yaxus-model/src/engine/mod.rs:530-551 over
 // Model::forward, crates/yaxus-model/src/lib.rs:434-453). Prints one JSON line:
 // host time per step (allocator + pass upload), whole-step time, and device time for
-// the attention launches alone.
+// the attention launches alone. A third loop runs each layer as the Rust crate's
+// Backend::attention does over a wrapped host backend (crates/yaxus-backend-hip/src/
+// lib.rs): the layer's qkv copied to the device, yx_attention_qkv_dev, the output
+// copied back (synchronous copies, from and to pageable memory, then through pinned
+// staging), against the same layer with device-resident qkv and output: the
+// per-layer cost of the host round trip.
 //
 // Usage: decode_loop [steps] [batch] [context] [layers]
 #include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <vector>
 
 #include "../../include/yaxus_hip.h"
@@ -44,7 +50,7 @@ int main(int argc, char** argv) {
   const size_t ctx_len = argc > 3 ? std::strtoul(argv[3], nullptr, 10) : 4000;
   const size_t layers = argc > 4 ? std::strtoul(argv[4], nullptr, 10) : 24;
   const size_t page = 16, hq = 16, hkv = 4, d = 128;
-  const size_t pages = B * ((ctx_len + 2 * steps + 8) / page + 2) + 16;  // tokens of both loops
+  const size_t pages = B * ((ctx_len + 3 * steps + 12) / page + 2) + 16;  // tokens of the three loops
 
   yx_cache* cache = nullptr;
   KVCHECK(yx_cache_create(pages, 1 << 20, page, &cache));
@@ -173,6 +179,58 @@ int main(int argc, char** argv) {
     tprev = tn;
   }
 
+  // The Rust crate's Backend::attention: qkv from host memory, output to host memory.
+  const size_t qkv_floats = B * (hq + 2 * hkv) * d, rope_len = ctx_len + 3 * steps + 64;
+  void *qkv, *qn, *kn, *rope, *out2;
+  HIPCHECK(yx_dev_alloc(ctx, qkv_floats * 4, &qkv));
+  HIPCHECK(yx_dev_alloc(ctx, d * 4, &qn));
+  HIPCHECK(yx_dev_alloc(ctx, d * 4, &kn));
+  HIPCHECK(yx_dev_alloc(ctx, rope_len * d * 4, &rope));
+  HIPCHECK(yx_dev_alloc(ctx, B * hq * d * 4, &out2));
+  HIPCHECK(yx_fill_normal(ctx, qkv, qkv_floats, YX_DTYPE_F32, 9, 0));
+  HIPCHECK(yx_fill_normal(ctx, qn, d, YX_DTYPE_F32, 9, 1ull << 32));
+  HIPCHECK(yx_fill_normal(ctx, kn, d, YX_DTYPE_F32, 9, 2ull << 32));
+  HIPCHECK(yx_fill_normal(ctx, rope, rope_len * d, YX_DTYPE_F32, 9, 3ull << 32));
+  std::vector<float> host_qkv(qkv_floats), host_out(B * hq * d);
+  HIPCHECK(yx_memcpy_d2h(ctx, host_qkv.data(), qkv, qkv_floats * 4));
+  void *pin_in, *pin_out;
+  HIPCHECK(yx_host_alloc(ctx, qkv_floats * 4, &pin_in));
+  HIPCHECK(yx_host_alloc(ctx, B * hq * d * 4, &pin_out));
+  std::vector<double> rt_layer_us, dev_layer_us, pin_layer_us;
+  for (int it = 0; it < steps + 3; ++it) {
+    prepare();
+    HIPCHECK(yx_sync(ctx));
+    for (size_t l = 0; l < layers; ++l) {
+      const auto a = clk::now();
+      HIPCHECK(yx_memcpy_h2d(ctx, qkv, host_qkv.data(), qkv_floats * 4));
+      HIPCHECK(yx_attention_qkv_dev(ctx, kv, l, static_cast<float*>(qkv), static_cast<float*>(qn),
+                                    static_cast<float*>(kn), static_cast<float*>(rope), rope_len, 1e-6f,
+                                    static_cast<float*>(out2), hq, hkv, 0, scale));
+      HIPCHECK(yx_memcpy_d2h(ctx, host_out.data(), out2, B * hq * d * 4));
+      const auto b = clk::now();
+      HIPCHECK(yx_attention_qkv_dev(ctx, kv, l, static_cast<float*>(qkv), static_cast<float*>(qn),
+                                    static_cast<float*>(kn), static_cast<float*>(rope), rope_len, 1e-6f,
+                                    static_cast<float*>(out2), hq, hkv, 0, scale));
+      HIPCHECK(yx_sync(ctx));
+      const auto c = clk::now();
+      // The same through pinned staging: the host qkv copied into pinned memory, DMA
+      // both ways, the output copied out of it.
+      std::memcpy(pin_in, host_qkv.data(), qkv_floats * 4);
+      HIPCHECK(yx_memcpy_h2d(ctx, qkv, pin_in, qkv_floats * 4));
+      HIPCHECK(yx_attention_qkv_dev(ctx, kv, l, static_cast<float*>(qkv), static_cast<float*>(qn),
+                                    static_cast<float*>(kn), static_cast<float*>(rope), rope_len, 1e-6f,
+                                    static_cast<float*>(out2), hq, hkv, 0, scale));
+      HIPCHECK(yx_memcpy_d2h(ctx, pin_out, out2, B * hq * d * 4));
+      std::memcpy(host_out.data(), pin_out, B * hq * d * 4);
+      const auto e = clk::now();
+      if (it >= 3) {
+        rt_layer_us.push_back(std::chrono::duration<double, std::micro>(b - a).count());
+        dev_layer_us.push_back(std::chrono::duration<double, std::micro>(c - b).count());
+        pin_layer_us.push_back(std::chrono::duration<double, std::micro>(e - c).count());
+      }
+    }
+  }
+
   float ms = 0;
   HIPCHECK(yx_timer_start(ctx));
   for (size_t l = 0; l < layers; ++l)
@@ -183,10 +241,15 @@ int main(int argc, char** argv) {
               "\"allocator_us_median\": %.1f, \"pass_begin_us_median\": %.1f, "
               "\"first_layer_call_us_median\": %.1f, \"other_layer_calls_us_median\": %.1f, "
               "\"step_us_median\": %.1f, \"overlapped_step_us_median\": %.1f, "
-              "\"attention_us_all_layers\": %.1f}\n",
+              "\"attention_us_all_layers\": %.1f, \"host_roundtrip_layer_us_median\": %.1f, "
+              "\"host_roundtrip_pinned_layer_us_median\": %.1f, "
+              "\"device_layer_us_median\": %.1f, \"qkv_bytes_h2d\": %zu, \"out_bytes_d2h\": %zu}\n",
               B, ctx_len, layers, median(host_us), median(alloc_us), median(pass_us), median(first_us),
-              median(launch_us), median(step_us), median(over_us), ms * 1000.0);
-  for (void* p : {q, k, v, out}) yx_dev_free(ctx, p);
+              median(launch_us), median(step_us), median(over_us), ms * 1000.0, median(rt_layer_us),
+              median(pin_layer_us), median(dev_layer_us), qkv_floats * 4, B * hq * d * 4);
+  for (void* p : {q, k, v, out, qkv, qn, kn, rope, out2}) yx_dev_free(ctx, p);
+  yx_host_free(ctx, pin_in);
+  yx_host_free(ctx, pin_out);
   yx_kv_destroy(ctx, kv);
   yx_ctx_destroy(ctx);
   yx_cache_destroy(cache);

@@ -168,9 +168,11 @@ def test_cfg5_verify_fork_rollback_decode(hip):
     """cfg5 in full: 16 requests of ctx 4096 (2048 shared) verify 5 draft tokens; 8 of
     them fork 3 tokens back (inside the partly filled tail page: copy on write of that
     page, in every layer); all 24 roll back a seeded count in [0, 5]; then one decode
-    step appends a token to each of the 24 sequences. Two layers, so the page copies are
-    seen in more than one layer."""
-    layers, pool = 2, 8192
+    step appends a token to each of the 24 sequences. All 24 layers of the configuration
+    (distinct arenas): the copy-on-write page copy is checked in every layer, and the
+    verify and the decode step after the rollback are checked against the oracle in
+    every layer."""
+    layers, pool = 24, 8192
     kv_ = _Both(pool)
     # The benchmark's scatter of the pool (bench._scatter), on both allocators.
     holders = [kv_.new_seq() for _ in range(pool)]

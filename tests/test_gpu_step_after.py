@@ -36,6 +36,38 @@ def test_matmul_bf16_matches_the_cpu_backend(hip, t, k, n):
     assert np.all(np.abs(got.astype(np.float64) - want) <= bound), np.abs(got - want).max()
 
 
+def test_matmul_bf16_at_the_ends_of_the_f32_range(hip):
+    """x near FLT_MAX (a rounded-up bf16 part would be inf), tiny x (down to 2^-110, the
+    low parts near bf16's subnormals) and infinite x (the CPU gives +-inf, not NaN), in
+    the same rows as ordinary values: within the same bound as above of the oracle, and
+    the same infinities."""
+    t, k, n = 4, 256, 48
+    x = normal(t * k, 41, 0).reshape(t, k)
+    x[0, :] *= np.float32(3.0e38) / np.abs(x[0, :]).max()    # |x| up to 3e38
+    x[0, ::2] = np.float32(3.4e38)                            # above bf16's largest (3.39e38)
+    x[1, :] *= np.float32(2.0 ** -100)
+    x[1, 5] = np.float32(2.0 ** -110) * np.float32(1.7)
+    x[2, 7] = np.inf
+    w = _bf16_bits(normal(n * k, 42, 0).reshape(n, k) * np.float32(2.0 ** -10))
+    w[:, 7] = _bf16_bits(np.float32(0.5))                     # row 2: +inf in every output
+    dx = hip.tensor(x.shape).upload(x)
+    dw = hip.tensor(w.shape, np.uint16).upload(w)
+    try:
+        got = hip.matmul_bf16(dx, dw).numpy()
+    finally:
+        dx.free()
+        dw.free()
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = matmul_bf16(x, w)
+    assert np.isfinite(got[[0, 1, 3]]).all()
+    assert np.array_equal(got[2], want[2]) and np.isposinf(got[2]).all()
+    wf = (w.astype(np.uint32) << 16).view(np.float32)
+    fin = [0, 1, 3]
+    bound = 2 * k * 2.0 ** -24 * (np.abs(x[fin]).astype(np.float64) @ np.abs(wf).astype(np.float64).T)
+    bound += k * 2.0 ** -149  # the subnormal floor of the f32 sums
+    assert np.all(np.abs(got[fin].astype(np.float64) - want[fin]) <= bound)
+
+
 def test_argmax_rows_matches_the_cpu_backend(hip):
     rng = np.random.default_rng(9)
     cases = [rng.standard_normal((16, 151936), dtype=np.float32),

@@ -91,6 +91,8 @@ HIP_SYMBOLS = {
     "yx_attention_append_noalloc": (I, [P, P, S, P, P, P, P, S, S, S, F]),
     "yx_dev_alloc": (I, [P, S, P]),
     "yx_dev_free": (I, [P, P]),
+    "yx_host_alloc": (I, [P, S, P]),
+    "yx_host_free": (I, [P, P]),
     "yx_memcpy_h2d": (I, [P, P, P, S]),
     "yx_memcpy_d2h": (I, [P, P, P, S]),
     "yx_dev_copy": (I, [P, P, P, S]),

@@ -357,6 +357,7 @@ struct yx_ctx {
   // 2: the 16-row-tile kernel for every decode pass.
   long decode_shape = 0;
   long cascade = 1;  // attend keys shared by consecutive groups (same pages) once for all of them
+  long xcd_prefix = 1;  // place the readers of one shared-prefix chunk on one XCD
   long prefill_split = 1;  // split long prefill tiles along keys when the pass underfills the GPU
   long matmul_k_split = 0;  // workgroups per matmul output tile along k (0: automatic)
   long argmax_slices = 0;   // workgroups per argmax row (0: automatic)
@@ -879,6 +880,43 @@ int build_plan(yx_ctx* c, size_t window, size_t hq, size_t hkv, bool f32, size_t
     const uint32_t total = nch + (s.casc >= 0 ? casc_nch[s.casc] : 0);
     if (total > 1) slot += nch;
   }
+  // XCD placement of shared prefixes: the GPU deals a launch's workgroups to its 8 XCDs
+  // (each with its own L2) in turn, x fastest, so items x and x' of one KV head run on
+  // one XCD when x = x' (mod 8). The prefix items reading the same chunk of a shared
+  // prefix (chunk j of every prefix group of that prefix's run) take positions
+  // = j (mod 8), so they share one L2 and the chunk comes from HBM once, not once per
+  // XCD they landed on. The other items fill the remaining positions in their order.
+  if (!cascs.empty() && c->xcd_prefix) {
+    const size_t n = plan.items.size();
+    std::vector<yx::AttnItem> placed(n);
+    std::vector<char> taken(n, 0), moved(n, 0);
+    size_t cursor[8] = {0, 1, 2, 3, 4, 5, 6, 7};
+    bool ok = true;
+    for (size_t i = 0; i < n && ok; ++i) {
+      const yx::AttnItem& w = plan.items[i];
+      if (!(w.pref_info & yx::kPrefixItem)) continue;
+      const uint32_t r = w.chunk % 8;
+      while (cursor[r] < n && taken[cursor[r]]) cursor[r] += 8;
+      if (cursor[r] >= n) {
+        ok = false;
+        break;
+      }
+      placed[cursor[r]] = w;
+      taken[cursor[r]] = 1;
+      moved[i] = 1;
+      cursor[r] += 8;
+    }
+    if (ok) {
+      size_t pos = 0;
+      for (size_t i = 0; i < n; ++i) {
+        if (moved[i]) continue;
+        while (taken[pos]) ++pos;
+        placed[pos] = plan.items[i];
+        taken[pos] = 1;
+      }
+      plan.items = std::move(placed);
+    }
+  }
   // The fused append needs each group in one sub and the last chunk of each group to
   // hold all of its rows' keys (the first row's position is the smallest).
   plan.fusable = true;
@@ -1276,6 +1314,7 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
   if (!c || !key) return fail(YX_ERR_INVALID, "null argument");
   if (value < 0 || (value == 0 && std::strcmp(key, "attn_target_waves") &&
                     std::strcmp(key, "attn_decode_shape") && std::strcmp(key, "attn_cascade") &&
+                    std::strcmp(key, "attn_xcd_prefix") &&
                     std::strcmp(key, "prefill_split") && std::strcmp(key, "prefill_min_rows") &&
                     std::strcmp(key, "matmul_k_split") && std::strcmp(key, "argmax_slices") &&
                     std::strcmp(key, "prefill_f32_waves")))
@@ -1292,6 +1331,8 @@ int yx_ctx_set_option(yx_ctx* c, const char* key, long value) {
     c->prefill_min_rows = value;
   else if (!std::strcmp(key, "attn_max_chunk_blocks"))
     c->max_chunk_blocks = value;
+  else if (!std::strcmp(key, "attn_xcd_prefix"))
+    c->xcd_prefix = value;
   else if (!std::strcmp(key, "attn_cascade"))
     c->cascade = value ? 1 : 0;
   else if (!std::strcmp(key, "prefill_split"))
@@ -1796,6 +1837,23 @@ int yx_dev_free(yx_ctx* c, void* p) {
   if (rc) return rc;
   YX_HIP(hipStreamSynchronize(c->stream));
   if (p) YX_HIP(hipFree(p));
+  return YX_OK;
+}
+
+int yx_host_alloc(yx_ctx* c, size_t bytes, void** out) {
+  if (!c || !out) return fail(YX_ERR_INVALID, "null argument");
+  int rc = c->set_device();
+  if (rc) return rc;
+  YX_HIP(hipHostMalloc(out, std::max<size_t>(bytes, 1), hipHostMallocDefault));
+  return YX_OK;
+}
+
+int yx_host_free(yx_ctx* c, void* p) {
+  if (!c) return fail(YX_ERR_INVALID, "null context");
+  int rc = c->set_device();
+  if (rc) return rc;
+  YX_HIP(hipStreamSynchronize(c->stream));
+  if (p) YX_HIP(hipHostFree(p));
   return YX_OK;
 }
 

@@ -7,8 +7,11 @@
 // output columns (weight rows) and 16 activation rows; its 8 waves take eighths of K and
 // their partial tiles are added in wave order (fixed, so the bits do not depend on
 // timing). Per 32 k, one v_mfma_f32_16x16x32_bf16 per part of x: the weight is bf16
-// exactly, and x goes in as three bf16 parts (hi, mid, lo: together the 24 bits of an
-// f32 significand), so every product is exact and only the f32 accumulation rounds.
+// exactly, and x goes in as three bf16 parts (hi, mid, lo: the 24 bits of an f32
+// significand cut in three by truncation), so every product is exact and only the f32
+// accumulation rounds. Range: exact for every finite x whose last significand bits stay
+// within bf16's (= f32's) exponent range, i.e. |x| >= 2^-110; below that the low parts
+// fall under the smallest subnormal (those x contribute below 2^-110 * |w| per term).
 //   A (weight): lane (c, g) holds w[n0 + c][k + 8g .. k + 8g + 7]
 //   B (x part): lane (c, g) holds x[t0 + c][k + 8g .. k + 8g + 7]
 //   D: lane (c, g) holds out[t0 + c][n0 + 4g + i], i = 0..3
@@ -81,10 +84,16 @@ __global__ __launch_bounds__(64 * kMmWaves) void matmul_bf16_rows(const float* _
       bf16x8 hi, mid, lo;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        hi[e] = static_cast<__bf16>(v[e]);
-        const float r1 = v[e] - static_cast<float>(hi[e]);
-        mid[e] = static_cast<__bf16>(r1);
-        lo[e] = static_cast<__bf16>(r1 - static_cast<float>(mid[e]));
+        // Truncated parts: hi = the top 8 significand bits, mid the next 8, lo the last
+        // 8, each difference exact. A finite x never rounds up to inf (x near FLT_MAX),
+        // and an infinite x is carried by hi alone (no inf - inf).
+        const float xh = __uint_as_float(__float_as_uint(v[e]) & 0xffff0000u);
+        const bool fin = __builtin_isfinite(v[e]);
+        const float r1 = fin ? v[e] - xh : 0.0f;
+        const float xm = __uint_as_float(__float_as_uint(r1) & 0xffff0000u);
+        hi[e] = static_cast<__bf16>(xh);
+        mid[e] = static_cast<__bf16>(xm);
+        lo[e] = static_cast<__bf16>(r1 - xm);
       }
       const bf16x8 a = __builtin_bit_cast(bf16x8, wv[u]);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, hi, acc, 0, 0, 0);
