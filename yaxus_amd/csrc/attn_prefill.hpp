@@ -146,6 +146,24 @@ __device__ __forceinline__ void load_to_lds16(const void* src, uint32_t lds) {
       : "memory");
 }
 
+// Keeps a value's computation at this point of the instruction stream: the empty asm
+// consumes and redefines the register, so the arithmetic that produces it cannot be sunk
+// past here (towards its first real use) by the compiler's code motion. The pair step
+// below uses it to keep its softmax slices between the matrix products they are meant to
+// overlap with.
+template <typename T>
+__device__ __forceinline__ void pin(T& v) {
+  __asm__ volatile("" : "+v"(v));
+}
+
+// max(a, b, c) in one instruction (fmaxf would first quiet each MFMA result with a
+// self-max of its own; scores are never signalling NaNs).
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // W waves of NT MFMA tiles each (W * NT * 16 = kPrefillRows logical rows) over stages of
 // SBT blocks; 8 / W waves per SIMD (an 8-wave workgroup fills a CU; two 4-wave ones share
 // it). Each wave overlaps its own matrix products with its softmax arithmetic
@@ -349,16 +367,21 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
     wlo = min(wlo, __builtin_amdgcn_readfirstlane(lo));
   }
 
-  // Running maxima start at a finite floor far below any score instead of -inf: a masked
-  // score (-inf) then always gives P = 0, a column that has seen no key yet keeps P = 0,
-  // and its first key rescales (by 2^(floor - s) = 0) the zero state, with no special
-  // cases. Scores are in log2 units of q.k / sqrt(d), far above the floor.
-  constexpr float kFloor = -1.0e30f;
-  float m[NT], lsum[NT];  // lsum: this lane's share of its column's sum (its 8 keys of every pair)
+  // Per column the running maximum m (log2 units of q.k / sqrt(d)), kept in the score
+  // accumulators' starting value: the score MFMAs of a pair start from -m, so they return
+  // x = s - m directly and the exponentials need no subtraction. A column that has seen
+  // no key yet has m = 0 (its x are the raw scores, exact) and threshold thr = -inf, so
+  // its first visible key triggers the (wave-uniform) move below; after that thr =
+  // kLazyRescale: m moves only when some x exceeds it, so P = 2^x stays below
+  // 2^kLazyRescale, well inside binary16 and f32, and the sum uses the same offset.
+  float m[NT], thr[NT], lsum[NT];  // lsum: this lane's share of its column's sum (its 8 keys of every pair)
+  floatx4 negm[NT];
   floatx4 acc[NT][8];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    m[t] = kFloor;
+    m[t] = 0.0f;
+    thr[t] = -INFINITY;
+    negm[t] = floatx4{0, 0, 0, 0};
     lsum[t] = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[t][j] = floatx4{0, 0, 0, 0};
@@ -461,86 +484,98 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
     for (int h = 0; h < 2; ++h)
       sc[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk[h][p], part ? ql[t][p] : qh[t][p], sc[t][h], 0, 0, 0);
   };
-  // Maxima of pair i (part one of its online softmax): masked scores, then, when some
-  // column's maximum grew by more than kLazyRescale (wave-uniform, rare after the first
-  // pairs), the accumulators and sums are rescaled in place and the maximum moves.
-  // Between moves, scores may exceed the maximum by up to kLazyRescale, so P stays
-  // below 2^kLazyRescale, well inside binary16 and f32; the sum uses the same offset, so
-  // the softmax is the same.
-  auto maxima_tile = [&](auto masked, int i, const floatx4 (&sc)[NT][2], float (&x)[NT][8], float (&mn)[NT],
+  float x[NT][8];  // the current pair's masked x = s - m
+  // Maxima of pair i (part one of its online softmax): masked x, and per lane the largest
+  // of its 8. When some lane's exceeds its column's threshold (wave-uniform, rare after
+  // a column's first keys), the column maxima move (`rescale`).
+  auto maxima_tile = [&](auto masked, int i, const floatx4 (&sc)[NT][2], float (&x)[NT][8], float (&bm)[NT],
                          int t) __attribute__((always_inline)) {
     const int key0 = first_key + 32 * i;
-    {
-      float bmax = kFloor;
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          if constexpr (decltype(masked)::value) {
-            const int kp = key0 + h * 16 + 4 * g + ii;
-            // Bitwise, not short-circuit: straight-line selects instead of branches.
-            const bool ok = (kp >= rlo[t]) & (kp <= rpos[t]) & (kp < key_end);
-            x[t][h * 4 + ii] = ok ? sc[t][h][ii] : -INFINITY;
-          } else {
-            x[t][h * 4 + ii] = sc[t][h][ii];
-          }
-          bmax = fmaxf(bmax, x[t][h * 4 + ii]);
+      for (int ii = 0; ii < 4; ++ii) {
+        if constexpr (decltype(masked)::value) {
+          const int kp = key0 + h * 16 + 4 * g + ii;
+          // Bitwise, not short-circuit: straight-line selects instead of branches.
+          const bool ok = (kp >= rlo[t]) & (kp <= rpos[t]) & (kp < key_end);
+          x[t][h * 4 + ii] = ok ? sc[t][h][ii] : -INFINITY;
+        } else {
+          x[t][h * 4 + ii] = sc[t][h][ii];
         }
-      mn[t] = fmaxf(m[t], max_xor32(max_xor16(bmax)));
-    }
+      }
+    bm[t] = max3(max3(max3(x[t][0], x[t][1], x[t][2]), x[t][3], x[t][4]), x[t][5], max3(x[t][6], x[t][7], x[t][7]));
+    pin(bm[t]);
   };
-  auto maxima = [&](auto masked, int i, const floatx4 (&sc)[NT][2], float (&x)[NT][8], float (&mn)[NT]) __attribute__((always_inline)) {
+  auto maxima = [&](auto masked, int i, const floatx4 (&sc)[NT][2], float (&x)[NT][8], float (&bm)[NT]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) maxima_tile(masked, i, sc, x, mn, t);
+    for (int t = 0; t < NT; ++t) maxima_tile(masked, i, sc, x, bm, t);
   };
-  auto rescale = [&](const float (&mn)[NT]) __attribute__((always_inline)) {
+  // The move: every column of the tile takes delta = max(0, its largest x) (a column's
+  // first keys: their largest x, m being 0 until then), so that m becomes the running
+  // maximum of its scores whenever some column's grew by more than kLazyRescale; the
+  // accumulator and sum are scaled by 2^-delta (zero state for a first move) and the
+  // pair's x shifted. A column still without a visible key keeps m = 0 and thr = -inf.
+  auto rescale = [&](const float (&bm)[NT], float (&x)[NT][8]) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      if (__builtin_amdgcn_ballot_w64(mn[t] > m[t] + kLazyRescale)) {  // wave-uniform
-        const float corr = __builtin_amdgcn_exp2f(m[t] - mn[t]);
+      if (__builtin_amdgcn_ballot_w64(bm[t] > thr[t])) {  // wave-uniform
+        const float cm = max_xor32(max_xor16(bm[t]));
+        const bool unset = thr[t] < 0.0f;
+        const float delta = unset ? (cm > -INFINITY ? cm : 0.0f) : fmaxf(0.0f, cm);
+        if (!(unset && cm == -INFINITY)) thr[t] = kLazyRescale;
+        const float corr = __builtin_amdgcn_exp2f(-delta);
         lsum[t] *= corr;
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[t][j] *= corr;
-        m[t] = mn[t];
+        m[t] += delta;
+        negm[t] = floatx4{-m[t], -m[t], -m[t], -m[t]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[t][e] -= delta;
       }
     }
   };
-  // Part two of pair i's softmax, in 24 slices per tile of 1-3 VALU each: P (element e
-  // of a lane is key (e / 4) * 16 + 4 g + e % 4 of the pair) as f16 hi + lo parts, and
-  // the sum. Slices 0-7 exponentials, 8-11 hi parts, 12-15 hi parts back to f32, 16-19 lo
-  // parts, 20-23 the sum.
+  // Part two of pair i's softmax, in slices of 1-2 VALU each: P = 2^x (element e of a
+  // lane is key (e / 4) * 16 + 4 g + e % 4 of the pair) as an f16 hi part and an f16 lo
+  // part, and the sum. The lo part takes two mixed-precision fmas per element pair: lo =
+  // f16(P - f32(hi)), a single rounding of the exact difference. Each slice pins its
+  // inputs and outputs where it is called, so the compiler keeps it between the matrix
+  // products it is meant to overlap (on gfx950 only about one VALU instruction per
+  // 16x16x32 MFMA issues for free; every further one adds its own issue time).
   struct Soft {
     float pr[NT][8];
-    floatx2 hf[NT][4];
     half8 ph[NT], pl[NT];
     float rs[NT];
   };
-  constexpr int kSlices = 24;
-  auto soft_slice = [&](int k, Soft& sf, const float (&x)[NT][8]) __attribute__((always_inline)) {
-    const int t = k / kSlices, sl = k % kSlices;
-    if (t >= NT) return;
-    if (sl < 8) {
-      sf.pr[t][sl] = __builtin_amdgcn_exp2f(x[t][sl] - m[t]);
-    } else if (sl < 12) {
-      const int e = sl - 8;
-      const half2_t h2 = __builtin_convertvector(floatx2{sf.pr[t][2 * e], sf.pr[t][2 * e + 1]}, half2_t);
-      sf.ph[t][2 * e] = h2[0];
-      sf.ph[t][2 * e + 1] = h2[1];
-    } else if (sl < 16) {
-      const int e = sl - 12;
-      sf.hf[t][e] = __builtin_convertvector(half2_t{sf.ph[t][2 * e], sf.ph[t][2 * e + 1]}, floatx2);
-    } else if (sl < 20) {
-      const int e = sl - 16;
-      const floatx2 d = floatx2{sf.pr[t][2 * e], sf.pr[t][2 * e + 1]} - sf.hf[t][e];
-      const half2_t l2 = __builtin_convertvector(d, half2_t);
-      sf.pl[t][2 * e] = l2[0];
-      sf.pl[t][2 * e + 1] = l2[1];
-    } else {
-      const int e = sl - 20;
-      const float r2 = sf.pr[t][2 * e] + sf.pr[t][2 * e + 1];
-      sf.rs[t] = e == 0 ? r2 : sf.rs[t] + r2;
-      if (e == 3) lsum[t] += sf.rs[t];
-    }
+  auto slice_exp = [&](Soft& sf, int t, int e) __attribute__((always_inline)) {
+    pin(x[t][e]);
+    sf.pr[t][e] = __builtin_amdgcn_exp2f(x[t][e]);
+    pin(sf.pr[t][e]);
+  };
+  auto slice_hi = [&](Soft& sf, int t, int e) __attribute__((always_inline)) {
+    const half2_t h2 = __builtin_convertvector(floatx2{sf.pr[t][2 * e], sf.pr[t][2 * e + 1]}, half2_t);
+    sf.ph[t][2 * e] = h2[0];
+    sf.ph[t][2 * e + 1] = h2[1];
+    pin(sf.ph[t]);
+  };
+  auto slice_lo = [&](Soft& sf, int t, int e) __attribute__((always_inline)) {
+    const uint32_t hp = __builtin_bit_cast(uint32_t, half2_t{sf.ph[t][2 * e], sf.ph[t][2 * e + 1]});
+    uint32_t lp;
+    __asm__ volatile(
+        "v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, %1, -1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=&v"(lp)
+        : "v"(hp), "v"(sf.pr[t][2 * e]), "v"(sf.pr[t][2 * e + 1]));
+    const half2_t l2 = __builtin_bit_cast(half2_t, lp);
+    sf.pl[t][2 * e] = l2[0];
+    sf.pl[t][2 * e + 1] = l2[1];
+  };
+  auto slice_sum = [&](Soft& sf, int t, int e) __attribute__((always_inline)) {
+    pin(sf.pr[t][2 * e]);
+    const float r2 = sf.pr[t][2 * e] + sf.pr[t][2 * e + 1];
+    sf.rs[t] = e == 0 ? r2 : sf.rs[t] + r2;
+    if (e == 3) lsum[t] += sf.rs[t];
+    pin(sf.rs[t]);
   };
   // O^T += V^T P^T for tile t, dim group j (hi product; lo product with lo = true).
   auto pv_mfma = [&](const half8 (&va)[8], const Soft& sf, int t, int j, bool lo) __attribute__((always_inline)) {
@@ -549,20 +584,18 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
 
   // One pair step, software-pipelined one pair ahead in both LDS reads and scores. On
-  // entry: pair i + 1's K is in kk, pair i's V in va, pair i's masked scores in x (its
-  // rescale done). Block one: pair i + 1's 16 * NT score MFMAs, each followed by a slice
-  // of pair i's softmax (exponentials, P parts, sums) and, every 16 / (16 NT / 16) MFMAs,
-  // one of pair i + 1's V reads (into vn): the wave issues in order, and an MFMA waiting
-  // for the busy matrix pipe holds back everything behind it, so each one carries some
-  // vector and LDS work. Halfway (even i), the next stage is entered. Block two: pair
-  // i's 16 * NT product MFMAs, interleaved with pair i + 1's maxima and pair i + 2's K
-  // reads (into kk). Then pair i + 1's rescale, if its maximum moved.
-  float x[NT][8];
+  // entry: pair i + 1's K is in kk, pair i's V in va, pair i's masked x (its rescale
+  // done). Block one: pair i + 1's 16 * NT score MFMAs (starting from -m), with pair i's
+  // exponentials and hi parts between them and pair i + 1's V reads (into vn). Halfway,
+  // the next stage is entered. Block two: pair i's 8 * NT hi products with its lo parts
+  // and pair i + 2's K reads (into kk) between them, then its 8 * NT lo products with its
+  // sums and pair i + 1's maxima between them. Then pair i + 1's rescale, if some column's
+  // maximum moved.
   half8 kk[2][4];
   auto step = [&](auto next_masked, int i, half8 (&va)[8], half8 (&vn)[8]) __attribute__((always_inline)) {
     floatx4 scn[NT][2];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) scn[t][0] = scn[t][1] = floatx4{0, 0, 0, 0};
+    for (int t = 0; t < NT; ++t) scn[t][0] = scn[t][1] = negm[t];
     Soft sf;
     constexpr int kMm = 16 * NT;  // score MFMAs
 #pragma unroll
@@ -570,35 +603,61 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
       const int k = q / (2 * NT), t = (q / 2) % NT, h = q % 2;
       const int part = k >> 2, p = k & 3;
       scn[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk[h][p], part ? ql[t][p] : qh[t][p], scn[t][h], 0, 0, 0);
+      // 12 slices per tile over the 16 * NT products: the exponentials first, then
+      // each hi pair once both of its exponentials are done.
 #pragma unroll
-      for (int sl = (q * kSlices * NT) / kMm; sl < ((q + 1) * kSlices * NT) / kMm; ++sl) soft_slice(sl, sf, x);
+      for (int sl = (q * 12 * NT) / kMm; sl < ((q + 1) * 12 * NT) / kMm; ++sl) {
+        if (sl % 12 < 8) slice_exp(sf, sl / 12, sl % 12);
+        else slice_hi(sf, sl / 12, sl % 12 - 8);
+      }
       if (q % (kMm / 8) == kMm / 8 - 1) read_v1(i + 1, vn, q / (kMm / 8));
       fence();
     }
     enter_mid(i);
-    const bool k_ahead = i + 2 < pb;
-    float mnn[NT];
+    float bmn[NT];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) pv_mfma(va, sf, t, j, false);
-      if (k_ahead) read_k1(i + 2, kk, j);
-      // The next pair's maxima, tile by tile, between the hi products.
-      if (j % (8 / NT) == 8 / NT - 1) maxima_tile(next_masked, i + 1, scn, x, mnn, j / (8 / NT));
+      // Unconditional (a pair past the wave's range reads ring data it never uses), so
+      // the block stays one straight line of products and reads.
+      read_k1(i + 2, kk, j);
+#pragma unroll
+      for (int sl = (j * 4 * NT) / 8; sl < ((j + 1) * 4 * NT) / 8; ++sl) slice_lo(sf, sl / 4, sl % 4);
       fence();
     }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) pin(sf.pl[t]);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) pv_mfma(va, sf, t, j, true);
+#pragma unroll
+      for (int sl = (j * 4 * NT) / 8; sl < ((j + 1) * 4 * NT) / 8; ++sl) slice_sum(sf, sl / 4, sl % 4);
+      // The next pair's maxima, tile by tile, between the lo products.
+      if (j % (8 / NT) == 8 / NT - 1) {
+        const int t = j / (8 / NT);
+        pin(scn[t][0]);
+        pin(scn[t][1]);
+        maxima_tile(next_masked, i + 1, scn, x, bmn, t);
+      }
       fence();
     }
-    rescale(mnn);
+    rescale(bmn, x);
   };
   auto last = [&](int i, const half8 (&va)[8]) __attribute__((always_inline)) {
     Soft sf;
 #pragma unroll
-    for (int k = 0; k < kSlices * NT; ++k) soft_slice(k, sf, x);
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) slice_exp(sf, t, e);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) slice_hi(sf, t, e);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) slice_lo(sf, t, e);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) slice_sum(sf, t, e);
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -627,12 +686,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
         for (int t = 0; t < NT; ++t) qk_mfma(kk, sc, k, t);
       read_v(pa, vaA);
       if (pa + 1 < pb) read_k(pa + 1, kk);
-      float mn[NT];
+      float bm[NT];
       if (pa >= wa && pa < wb)
-        maxima(std::false_type{}, pa, sc, x, mn);
+        maxima(std::false_type{}, pa, sc, x, bm);
       else
-        maxima(std::true_type{}, pa, sc, x, mn);
-      rescale(mn);
+        maxima(std::true_type{}, pa, sc, x, bm);
+      rescale(bm, x);
     }
     // Steps by the kind of their next pair: masked before wa, whole in [wa, wb), masked
     // from wb. Two steps per turn, so that the V registers swap roles without copies.
