@@ -121,6 +121,23 @@ __device__ __forceinline__ void merge_tile(uint32_t r0, uint32_t nrows, uint32_t
   }
 }
 
+#ifdef YX_PF_PROF
+// Phase clocks of the prefill kernel, summed over waves (a profiling build only).
+// Slot [k][wave of the launch], overwritten by each launch.
+__device__ unsigned long long g_pf_prof[12][16384];
+#define PF_NOW() __builtin_amdgcn_s_memtime()
+#define PF_CYC(v) const uint64_t v = __builtin_amdgcn_s_memtime()
+#define PF_ACC(a, x, y) a += ((y) - (x))
+#define PF_ADD(k, v) \
+  if ((threadIdx.x & 63) == 0 && blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6) < 16384u) \
+    g_pf_prof[k][blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)] = static_cast<unsigned long long>(v)
+#else
+#define PF_NOW() 0ull
+#define PF_ADD(k, v)
+#define PF_CYC(v)
+#define PF_ACC(a, x, y)
+#endif
+
 static constexpr int kPrefillWaves = 4;
 static constexpr int kPrefillTiles = 1;  // MFMA tiles (16 logical rows) per wave
 static constexpr int kPrefillRows = kPrefillWaves * kPrefillTiles * 16;  // logical rows per item
@@ -164,6 +181,28 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
   return r;
 }
 
+// One block half (4 KiB: 4 rows of 1 KiB) from global memory straight into LDS: row r
+// comes from base + off[r % 2] + 1024 r (the lanes' 16-byte pieces) and lands at LDS
+// byte address lds + 1024 r (lane i's piece at + 16 i). The global address is the
+// scalar base plus a 32-bit lane offset; the instruction's immediate offset applies to
+// both the global and the LDS address, so M0 (the LDS address) is set once for the four
+// rows (its previous value is restored after). The loads count in vmcnt like any other;
+// callers wait for them explicitly (the compiler does not know about them).
+__device__ __forceinline__ void load_half_to_lds(const void* base, uint32_t off0, uint32_t off1, uint32_t lds) {
+  uint32_t saved;  // M0 is the compiler's
+  __asm__ volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %4\n\t"
+      "global_load_lds_dwordx4 %2, %1\n\t"
+      "global_load_lds_dwordx4 %3, %1 offset:1024\n\t"
+      "global_load_lds_dwordx4 %2, %1 offset:2048\n\t"
+      "global_load_lds_dwordx4 %3, %1 offset:3072\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(base), "v"(off0), "v"(off1), "s"(lds)
+      : "memory");
+}
+
 // W waves of NT MFMA tiles each (W * NT * 16 = kPrefillRows logical rows) over stages of
 // SBT blocks; 8 / W waves per SIMD (an 8-wave workgroup fills a CU; two 4-wave ones share
 // it). Each wave overlaps its own matrix products with its softmax arithmetic
@@ -188,6 +227,12 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   __shared__ half8 ring[kRing][2 * SB * 256];
   // One dimension, KV head fastest: workgroups start in the host's longest-first item
   // order across all KV heads.
+  const uint64_t pf_t0 = PF_NOW();
+#ifdef YX_PF_PROF
+  const uint64_t pf_r0 = __builtin_amdgcn_s_memrealtime();
+#endif
+  uint64_t pf_stage = 0, pf_rare = 0, pf_b0 = 0, pf_b1 = 0, pf_b2 = 0, pf_b3 = 0;
+  (void)pf_t0; (void)pf_stage; (void)pf_rare;
   const PrefillItem it = items[blockIdx.x / hkv];
   const uint32_t kh = blockIdx.x % hkv;
   const int tid = threadIdx.x;
@@ -209,45 +254,75 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   static_assert((2 * SB) % W == 0, "whole block halves per wave");
   constexpr int HW = 2 * SB / W;
   constexpr int kRowsPerWave = 4 * HW;  // 1 KiB rows (loads) per wave per stage
-  uint32_t src_k[4], src_v[4];
+  // Lane offsets of rows r = 0, 1 (rows 2 and 3 repeat them 2 KiB on).
+  uint32_t src_k[2], src_v[2];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
+  for (int r = 0; r < 2; ++r) {
     const uint32_t key = 4 * r + (lane >> 4), pp = lane & 15;
     src_v[r] = key * 256u + (2u * ((pp >> 1) ^ (key & 7u)) + (pp & 1u)) * 16u;
     src_k[r] = static_cast<uint32_t>(r * 1024 + ((lane & 15) * 4 + (lane >> 4)) * 16);
   }
   const uint32_t ring_base = static_cast<uint32_t>(
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) half8*)&ring[0][0]));
-  // The pages of the blocks a wave moves for stage st are read one stage ahead, so the
-  // scalar loads' latency is not waited for right after the stage's barrier.
-  auto page_of = [&](uint32_t st, uint32_t blk) __attribute__((always_inline)) {  // (page id, block within the page)
-    uint32_t b = it.blk0 + st * SB + blk;
-    b = b < it.blk1 ? b : it.blk1 - 1;  // past the end: re-read the last block (unused)
-    return uint2{pt[b >> bpp_shift], b & bpp_mask};
+  // The page ids of the block this wave moves, from an LDS table of two 64-stage batches
+  // per wave (lane l of a batch's load fetches stage 64 k + l's id straight into the
+  // table): batches 0 and 1 are loaded at the start, batch k + 1 when batch k comes into
+  // use, 64 stages before it is read. The loads count in vmcnt and are complete long
+  // before they are read (the stages' own waits pass them). Stages 0 and 1 take their ids
+  // from a scalar read of the page table; each later stage reads its id from the table one
+  // stage ahead, so the loop never waits for a page-table read in memory.
+  static_assert(HW == 1, "one block half per wave and stage");
+  __shared__ uint32_t pid_tab[W][2][64];
+  const uint32_t my_blk = static_cast<uint32_t>(wave >> 1);
+  const bool my_v = (wave & 1) != 0;
+  auto block_of = [&](uint32_t st) __attribute__((always_inline)) {  // past the end: the last block (unused)
+    const uint32_t b = it.blk0 + st * SB + my_blk;
+    return b < it.blk1 ? b : it.blk1 - 1;
   };
-  constexpr int BW = (HW + 1) / 2;  // blocks a wave touches per stage
-  uint2 next_page[BW];
-#pragma unroll
-  for (int bb = 0; bb < BW; ++bb) next_page[bb] = page_of(0, static_cast<uint32_t>((wave * HW) / 2 + bb));
-  auto issue = [&](uint32_t st, uint32_t slot) __attribute__((always_inline)) {  // stage st into ring slot `slot`
-    size_t elem[BW];
-#pragma unroll
-    for (int bb = 0; bb < BW; ++bb) {
-      elem[bb] = (static_cast<size_t>(next_page[bb].x) * hkv + kh) * head_stride +
-                 static_cast<size_t>(next_page[bb].y) * 16 * kD;
-      next_page[bb] = page_of(st + 1, static_cast<uint32_t>((wave * HW) / 2 + bb));
-    }
-#pragma unroll
-    for (int hh = 0; hh < HW; ++hh) {
-      const int h = wave * HW + hh;
-      const uint32_t my_blk = static_cast<uint32_t>(h >> 1);
-      const bool my_v = (h & 1) != 0;
-      const char* blk = reinterpret_cast<const char*>(my_v ? vc : kc) + elem[(hh + (wave * HW) % 2) / 2] * 2;
-      const uint32_t dst = ring_base + slot * (2 * SB * 256 * 16) + (my_v ? SB * 4096u : 0u) + my_blk * 4096u;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) load_to_lds16(blk + (my_v ? src_v[r] : src_k[r]), dst + r * 1024);
-    }
+  const uint32_t tab_base = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint32_t*)&pid_tab[wave][0][0]));
+  auto load_batch = [&](uint32_t k) __attribute__((always_inline)) {
+    const uint32_t* src = pt + (block_of(64u * k + static_cast<uint32_t>(lane)) >> bpp_shift);
+    uint32_t saved;
+    __asm__ volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dword %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(tab_base + (k & 1u) * 256u)
+        : "memory");
   };
+  auto tab_read = [&](uint32_t st) __attribute__((always_inline)) {
+    return pid_tab[wave][(st >> 6) & 1u][st & 63u];
+  };
+  // This wave's half of every block: K or V, its KV head's part of each page.
+  const char* const half_base = reinterpret_cast<const char*>(my_v ? vc : kc) + static_cast<size_t>(kh) * head_stride * 2;
+  const uint32_t page_bytes = static_cast<uint32_t>(hkv * head_stride * 2);
+  // Stages 0-2 take their ids from scalar reads of the page table, waited for at once (the
+  // batches' loads are only known complete after the first stage's wait); each later
+  // stage's id is read from the table during the stage before.
+  auto pt_at = [&](uint32_t st) __attribute__((always_inline)) {
+    return pt + __builtin_amdgcn_readfirstlane(block_of(st) >> bpp_shift);
+  };
+  uint32_t pid_pre;
+  auto issue_page = [&](uint32_t st, uint32_t slot, uint32_t page) __attribute__((always_inline)) {
+    const uint32_t blkin = block_of(st) & bpp_mask;
+    const char* blk = half_base + static_cast<uint64_t>(page) * page_bytes + blkin * 4096u;
+    const uint32_t dst = ring_base + slot * (2 * SB * 256 * 16) + (my_v ? SB * 4096u : 0u) + my_blk * 4096u;
+    if (my_v)
+      load_half_to_lds(blk, src_v[0], src_v[1] - 1024u, dst);
+    else
+      load_half_to_lds(blk, src_k[0], src_k[1] - 1024u, dst);
+  };
+  auto issue = [&](uint32_t st, uint32_t slot) __attribute__((always_inline)) {  // stage st >= 2 into ring slot `slot`
+    const uint32_t page = __builtin_amdgcn_readfirstlane(pid_pre);
+    if ((st & 63u) == 0) load_batch(st / 64u + 1u);  // wave-uniform, once per 64 stages
+    pid_pre = tab_read(st + 1);
+    issue_page(st, slot, page);
+  };
+  load_batch(0);
+  load_batch(1);
   // q and pos are read first, unconditionally (rows past the tile read row 0 and are
   // zeroed), so that waiting for them does not wait for the K/V stages issued after.
   // q and pos are not declared __restrict__ and the empty asm may write memory, so the
@@ -277,8 +352,20 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   __asm__ volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
   const uint32_t nst = (it.blk1 - it.blk0 + SB - 1) / SB;  // stages
-#pragma unroll
-  for (int j = 0; j < kLead; ++j) issue(j, j);
+  static_assert(kLead == 2, "stages 0 and 1 are issued first");
+  {
+    uint32_t p0, p1;
+    __asm__ volatile(
+        "s_load_dword %0, %3, 0x0\n\t"
+        "s_load_dword %1, %4, 0x0\n\t"
+        "s_load_dword %2, %5, 0x0\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(p0), "=&s"(p1), "=&s"(pid_pre)
+        : "s"(pt_at(0)), "s"(pt_at(1)), "s"(pt_at(2))
+        : "memory");
+    issue_page(0, 0, p0);
+    issue_page(1, 1, p1);
+  }
 
   if constexpr (QKV) {
     // write_rows for the columns' q heads. Lane g of a column holds dims
@@ -367,10 +454,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
     wlo = min(wlo, __builtin_amdgcn_readfirstlane(lo));
   }
 
+  // -FLT_MAX: the per-lane maximum of a pair whose keys are all masked (-inf); every
+  // visible key's x is above it.
+  constexpr float kNoKey = -3.40282347e38f;
   // Per column the running maximum m (log2 units of q.k / sqrt(d)), kept in the score
   // accumulators' starting value: the score MFMAs of a pair start from -m, so they return
   // x = s - m directly and the exponentials need no subtraction. A column that has seen
-  // no key yet has m = 0 (its x are the raw scores, exact) and threshold thr = -inf, so
+  // no key yet has m = 0 (its x are the raw scores, exact) and threshold thr = kNoKey, so
   // its first visible key triggers the (wave-uniform) move below; after that thr =
   // kLazyRescale: m moves only when some x exceeds it, so P = 2^x stays below
   // 2^kLazyRescale, well inside binary16 and f32, and the sum uses the same offset.
@@ -380,7 +470,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     m[t] = 0.0f;
-    thr[t] = -INFINITY;
+    thr[t] = kNoKey;
     negm[t] = floatx4{0, 0, 0, 0};
     lsum[t] = 0.0f;
 #pragma unroll
@@ -429,17 +519,35 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   // visible. Every wave has then also issued and (lgkmcnt) finished its reads of stage
   // st - 2, whose slot is refilled with stage st + kLead (the last pair of stage st - 1
   // still reads its V after the barrier).
+#ifdef YX_PF_PROF
+  uint64_t e0 = 0, e1 = 0, e2 = 0, e3 = 0, e4 = 0, pf_e1 = 0, pf_e2 = 0, pf_e3 = 0, pf_e4 = 0;
+#endif
   auto stage_enter = [&](uint32_t st) __attribute__((always_inline)) {
+#ifdef YX_PF_PROF
+    e0 = PF_NOW();
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    e1 = PF_NOW();
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(kRowsPerWave * (kLead - 1)) : "memory");
+    e2 = PF_NOW();
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    e3 = PF_NOW();
+    issue(st + kLead, (st + kLead) & (kRing - 1));
+    e4 = PF_NOW();
+#else
     __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)" ::"n"(kRowsPerWave * (kLead - 1))
                      : "memory");
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
     issue(st + kLead, (st + kLead) & (kRing - 1));
+#endif
   };
-  // The stage holding pair i + 2 is entered halfway through pair i (when pair i + 2 is
-  // the first pair of its stage), so that the second half of pair i can already read
-  // pair i + 2's K. Its slot's previous stage was last read in the first half of the
-  // pair after that stage's last pair, which every wave has passed: kLead <= kRing - 2.
+  // The stage holding pair i + 2 is entered at the start of pair i's step (when pair
+  // i + 2 is the first pair of its stage), so that the step can already read pair i + 2's
+  // K. The slot refilled then held pair i, whose K and V every wave has read into
+  // registers by then (the previous step read its V; lgkmcnt(0) before the barrier):
+  // kLead <= kRing - 2. At that point the wave's only LDS reads in flight are pair
+  // i + 1's K, which the step's first products need anyway.
   static_assert(kLead <= kRing - 2, "a refilled slot is no longer read");
   auto enter_mid = [&](int i) __attribute__((always_inline)) {
     const int j = i + 2;
@@ -504,7 +612,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
           x[t][h * 4 + ii] = sc[t][h][ii];
         }
       }
-    bm[t] = max3(max3(max3(x[t][0], x[t][1], x[t][2]), x[t][3], x[t][4]), x[t][5], max3(x[t][6], x[t][7], x[t][7]));
+    float b = kNoKey;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) b = fmaxf(b, x[t][e]);
+    bm[t] = b;
     pin(bm[t]);
   };
   auto maxima = [&](auto masked, int i, const floatx4 (&sc)[NT][2], float (&x)[NT][8], float (&bm)[NT]) __attribute__((always_inline)) {
@@ -515,15 +626,17 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   // first keys: their largest x, m being 0 until then), so that m becomes the running
   // maximum of its scores whenever some column's grew by more than kLazyRescale; the
   // accumulator and sum are scaled by 2^-delta (zero state for a first move) and the
-  // pair's x shifted. A column still without a visible key keeps m = 0 and thr = -inf.
+  // pair's x shifted. A column still without a visible key keeps m = 0 and thr = kNoKey.
   auto rescale = [&](const float (&bm)[NT], float (&x)[NT][8]) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       if (__builtin_amdgcn_ballot_w64(bm[t] > thr[t])) {  // wave-uniform
+        const uint64_t a = PF_NOW();
         const float cm = max_xor32(max_xor16(bm[t]));
         const bool unset = thr[t] < 0.0f;
-        const float delta = unset ? (cm > -INFINITY ? cm : 0.0f) : fmaxf(0.0f, cm);
-        if (!(unset && cm == -INFINITY)) thr[t] = kLazyRescale;
+        const bool seen = cm > kNoKey;
+        const float delta = unset ? (seen ? cm : 0.0f) : fmaxf(0.0f, cm);
+        if (seen) thr[t] = kLazyRescale;
         const float corr = __builtin_amdgcn_exp2f(-delta);
         lsum[t] *= corr;
 #pragma unroll
@@ -532,6 +645,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
         negm[t] = floatx4{-m[t], -m[t], -m[t], -m[t]};
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[t][e] -= delta;
+        pf_rare += PF_NOW() - a;
       }
     }
   };
@@ -593,6 +707,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   // maximum moved.
   half8 kk[2][4];
   auto step = [&](auto next_masked, int i, half8 (&va)[8], half8 (&vn)[8]) __attribute__((always_inline)) {
+    PF_CYC(c0);
+    enter_mid(i);
+    PF_CYC(c1);
+    __builtin_amdgcn_s_setprio(1);
     floatx4 scn[NT][2];
 #pragma unroll
     for (int t = 0; t < NT; ++t) scn[t][0] = scn[t][1] = negm[t];
@@ -613,8 +731,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
       if (q % (kMm / 8) == kMm / 8 - 1) read_v1(i + 1, vn, q / (kMm / 8));
       fence();
     }
-    enter_mid(i);
     float bmn[NT];
+    PF_CYC(c2);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
 #pragma unroll
@@ -628,6 +746,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) pin(sf.pl[t]);
+    PF_CYC(c3);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
 #pragma unroll
@@ -637,12 +756,19 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
       // The next pair's maxima, tile by tile, between the lo products.
       if (j % (8 / NT) == 8 / NT - 1) {
         const int t = j / (8 / NT);
-        pin(scn[t][0]);
-        pin(scn[t][1]);
         maxima_tile(next_masked, i + 1, scn, x, bmn, t);
       }
       fence();
     }
+    PF_CYC(c4);
+    __builtin_amdgcn_s_setprio(0);
+    PF_ACC(pf_b0, c0, c1);
+    PF_ACC(pf_b1, c1, c2);
+    PF_ACC(pf_b2, c2, c3);
+    PF_ACC(pf_b3, c3, c4);
+#ifdef YX_PF_PROF
+    pf_e1 += e1 - e0; pf_e2 += e2 - e1; pf_e3 += e3 - e2; pf_e4 += e4 - e3;
+#endif
     rescale(bmn, x);
   };
   auto last = [&](int i, const half8 (&va)[8]) __attribute__((always_inline)) {
@@ -670,6 +796,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   };
 
   stage_enter(0);  // pairs 0 .. PPS - 1
+  const uint64_t pf_t1 = PF_NOW();
+  (void)pf_t1;
   if (PPS == 1 && nst > 1) stage_enter(1);
   int i = 0;
   for (; i < pa; ++i) enter_mid(i);
@@ -716,6 +844,32 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
     ++i;
   }
   for (; i < npair; ++i) enter_mid(i);
+  const uint64_t pf_t2 = PF_NOW();
+  (void)pf_t2;
+  PF_ADD(1, pf_t1 - pf_t0);
+  PF_ADD(2, pf_t2 - pf_t1);
+  PF_ADD(3, pf_stage);
+  PF_ADD(4, pf_rare);
+  PF_ADD(6, 1);
+  PF_ADD(7, pb - pa);
+  PF_ADD(8, pf_b0);
+  PF_ADD(9, pf_b1);
+  PF_ADD(10, pf_b2);
+  PF_ADD(11, pf_b3);
+#ifdef YX_PF_PROF
+  PF_ADD(3, pf_e1);
+  PF_ADD(4, pf_e2);
+  PF_ADD(0, pf_e3);
+  PF_ADD(5, pf_e4);
+#endif
+#ifdef YX_PF_PROF
+  {
+    uint32_t hw, xcc;
+    __asm__ volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    __asm__ volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    (void)hw; (void)xcc;
+  }
+#endif
   // No load into LDS may land after the workgroup ends.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
@@ -736,6 +890,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
         *reinterpret_cast<float4*>(o + j * 16) =
             float4{acc[t][j][0] * inv, acc[t][j][1] * inv, acc[t][j][2] * inv, acc[t][j][3] * inv};
     }
+    (void)pf_t2;
+#ifdef YX_PF_PROF
+    (void)pf_r0;
+#endif
     return;
   }
   // A split tile: this chunk's (maximum, sum, unnormalised O) of each column go to its

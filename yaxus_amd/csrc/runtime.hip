@@ -1240,6 +1240,13 @@ extern "C" {
 
 const char* yx_last_error(void) { return g_err.c_str(); }
 
+#ifdef YX_PF_PROF
+// Profiling build only: reads and clears the prefill kernel's phase clocks.
+int yx_debug_pf_prof(unsigned long long* out) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(yx::g_pf_prof), sizeof(yx::g_pf_prof)) == hipSuccess ? 0 : 5;
+}
+#endif
+
 int yx_device_count(int* n) {
   YX_HIP(hipGetDeviceCount(n));
   return YX_OK;
