@@ -124,7 +124,7 @@ __device__ __forceinline__ void merge_tile(uint32_t r0, uint32_t nrows, uint32_t
 #ifdef YX_PF_PROF
 // Phase clocks of the prefill kernel, summed over waves (a profiling build only).
 // Slot [k][wave of the launch], overwritten by each launch.
-__device__ unsigned long long g_pf_prof[12][16384];
+__device__ unsigned long long g_pf_prof[16][16384];
 #define PF_NOW() __builtin_amdgcn_s_memtime()
 #define PF_CYC(v) const uint64_t v = __builtin_amdgcn_s_memtime()
 #define PF_ACC(a, x, y) a += ((y) - (x))
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
         : "s"(pt_at(0)), "s"(pt_at(1)), "s"(pt_at(2))
         : "memory");
     issue_page(0, 0, p0);
-    issue_page(1, 1, p1);
+    if (nst > 1) issue_page(1, 1, p1);
   }
 
   if constexpr (QKV) {
@@ -518,7 +518,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   // kLead - 1 later stages' are in flight, and the barrier makes every wave's part
   // visible. Every wave has then also issued and (lgkmcnt) finished its reads of stage
   // st - 2, whose slot is refilled with stage st + kLead (the last pair of stage st - 1
-  // still reads its V after the barrier).
+  // still reads its V after the barrier). Stages past the item's last are not loaded, so
+  // the last stage waits for every load, and the workgroup ends with none in flight.
 #ifdef YX_PF_PROF
   uint64_t e0 = 0, e1 = 0, e2 = 0, e3 = 0, e4 = 0, pf_e1 = 0, pf_e2 = 0, pf_e3 = 0, pf_e4 = 0;
 #endif
@@ -527,19 +528,25 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
     e0 = PF_NOW();
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     e1 = PF_NOW();
-    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(kRowsPerWave * (kLead - 1)) : "memory");
+    if (st + 1 < nst)
+      __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(kRowsPerWave * (kLead - 1)) : "memory");
+    else
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     e2 = PF_NOW();
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
     e3 = PF_NOW();
-    issue(st + kLead, (st + kLead) & (kRing - 1));
+    if (st + kLead < nst) issue(st + kLead, (st + kLead) & (kRing - 1));
     e4 = PF_NOW();
 #else
-    __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)" ::"n"(kRowsPerWave * (kLead - 1))
-                     : "memory");
+    if (st + 1 < nst)  // the next stage's loads may still be in flight
+      __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)" ::"n"(kRowsPerWave * (kLead - 1))
+                       : "memory");
+    else  // the last stage: nothing was issued after it
+      __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
-    issue(st + kLead, (st + kLead) & (kRing - 1));
+    if (st + kLead < nst) issue(st + kLead, (st + kLead) & (kRing - 1));
 #endif
   };
   // The stage holding pair i + 2 is entered at the start of pair i's step (when pair
@@ -795,7 +802,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
     enter_mid(i);
   };
 
+#ifdef YX_PF_PROF
+  __builtin_amdgcn_sched_barrier(0);
+  const uint64_t pf_rq = __builtin_amdgcn_s_memrealtime();
+#endif
   stage_enter(0);  // pairs 0 .. PPS - 1
+#ifdef YX_PF_PROF
+  const uint64_t pf_rs = __builtin_amdgcn_s_memrealtime();
+#endif
   const uint64_t pf_t1 = PF_NOW();
   (void)pf_t1;
   if (PPS == 1 && nst > 1) stage_enter(1);
@@ -857,17 +871,19 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
   PF_ADD(10, pf_b2);
   PF_ADD(11, pf_b3);
 #ifdef YX_PF_PROF
-  PF_ADD(3, pf_e1);
-  PF_ADD(4, pf_e2);
-  PF_ADD(0, pf_e3);
-  PF_ADD(5, pf_e4);
+  (void)pf_e1; (void)pf_e2; (void)pf_e3; (void)pf_e4;
+  PF_ADD(0, pf_rq);
+  PF_ADD(3, pf_rs);
+  PF_ADD(4, __builtin_amdgcn_s_memrealtime());
 #endif
 #ifdef YX_PF_PROF
   {
     uint32_t hw, xcc;
     __asm__ volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
     __asm__ volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-    (void)hw; (void)xcc;
+    PF_ADD(12, pf_r0);
+    PF_ADD(14, (static_cast<uint64_t>(xcc) << 32) | hw);
+    PF_ADD(15, (static_cast<uint64_t>(blockIdx.x) << 32) | static_cast<uint32_t>(npair));
   }
 #endif
   // No load into LDS may land after the workgroup ends.
@@ -892,7 +908,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(8 / W, 8
     }
     (void)pf_t2;
 #ifdef YX_PF_PROF
-    (void)pf_r0;
+    PF_ADD(5, __builtin_amdgcn_s_memrealtime());
+    __builtin_amdgcn_s_waitcnt(0);
+    PF_ADD(13, __builtin_amdgcn_s_memrealtime());
 #endif
     return;
   }
